@@ -1,0 +1,307 @@
+#!/usr/bin/env python
+"""Benchmark of the paged-KV attention path on one MI355X.
+
+Headline (the JSON line's `value`): paged decode at serving scale -- 256 sequences,
+Lk ~ U[1024, 8192], 16 q / 8 kv heads, head_dim 128, bf16, 256-key blocks from a
+shuffled pool. One step is one Attention.forward in decode mode: store_kvcache of
+the 256 new tokens, then paged decode attention over all 256 sequences. `value` is
+the KV bytes the step must read (sum Lk * 2 * 2048 B) divided by the measured step
+time, in GB/s; all inputs are resident in HBM before the timed region starts.
+
+`roofline` is the decode attention call alone, timed per launch with HIP events on
+the stream it is launched on. `cpu_baseline` is the CPU oracle (torch on all host
+cores) on a bounded sample of the same workload. `kernels` reports every other
+configuration (store, mixed chunked prefill + decode, shared-prefix decode).
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (ROOT / "nano-vllm-diy_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "paged decode attn KV GB/s (% HBM peak) + e2e gen tok/s, Qwen3-0.6B shape"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+SCALE = 128 ** -0.5
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_launches(fn, reps: int, warmup: int = 3):
+    """Mean and median GPU time (ms) of fn() measured with events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    ts = [a.elapsed_time(b) for a, b in evs]
+    return statistics.fmean(ts), statistics.median(ts)
+
+
+def attention_call(w, sub=None):
+    """Closure running the path's attention op on workload w (optionally a sub-batch)."""
+    import pagedkv
+
+    cu_q, cu_k, bt, mq, mk = w.cu_seqlens_q, w.cu_seqlens_k, w.block_tables, w.max_seqlen_q, w.max_seqlen_k
+    if sub is not None:
+        cu_q, cu_k, bt, mq, mk = sub
+    out = pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt)
+
+    def fn():
+        pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt, out=out)
+    return fn
+
+
+def sub_batch(w, keep):
+    """Metadata selecting only sequences `keep` (others padded to length 0)."""
+    import torch
+
+    q_lens = [lq if keep(i) else 0 for i, lq in enumerate(w.q_lens)]
+    k_lens = [lk if keep(i) else 0 for i, lk in enumerate(w.k_lens)]
+    # rows keep their positions in q: express skipped sequences as zero-length spans
+    cu_q, cu_k, a, c = [0], [0], 0, 0
+    for i, (lq, lk) in enumerate(zip(w.q_lens, w.k_lens)):
+        a += lq
+        c += lk
+        cu_q.append(a)
+        cu_k.append(c)
+    # a skipped sequence gets Lq = 0 by repeating the previous offset
+    cq, ck = [0], [0]
+    for i in range(len(w.q_lens)):
+        cq.append(cu_q[i + 1] if keep(i) else cu_q[i])
+        ck.append(ck[-1] + k_lens[i])
+        if not keep(i):
+            cq[-1] = cq[-2]
+    # q rows are addressed by cu_q[b]; skipped sequences have Lq = 0 so are never read,
+    # but kept sequences must still start at their own rows
+    cq = [0] + [cu_q[i + 1] if keep(i) else cu_q[i] for i in range(len(w.q_lens))]
+    starts = [cu_q[i] for i in range(len(w.q_lens))]
+    dev = w.q.device
+    # Build explicit start/end pairs: Lq_b = cq[b+1] - cq[b] must be the kept length and
+    # cq[b] must equal the sequence's first row. Use per-sequence (start, start + Lq).
+    ok = all(cq[i] == starts[i] or not keep(i) for i in range(len(starts)))
+    assert ok
+    return (torch.tensor(cq, dtype=torch.int32, device=dev), torch.tensor(ck, dtype=torch.int32, device=dev),
+            w.block_tables, max(q_lens), max(k_lens))
+
+
+def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
+    """Oracle (CPU torch, all cores) on the first max_seqs sequences of w: store + attention."""
+    import torch
+
+    import oracle  # CPU baseline leg only
+    sys.path.insert(0, str(ROOT / "tests"))
+    from paged_helpers import subset_oracle  # noqa: F401  (shares the block-subsetting logic)
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    ids = list(range(min(max_seqs, len(w.q_lens))))
+    import math
+
+    bt = w.block_tables.cpu()
+    blocks = sorted({int(x) for b in ids for x in bt[b, :math.ceil(w.k_lens[b] / 256)].tolist()})
+    remap = {old: new for new, old in enumerate(blocks)}
+    idx = torch.tensor(blocks, dtype=torch.long, device=w.k_cache.device)
+    kc0 = w.k_cache.index_select(0, idx).cpu()
+    vc0 = w.v_cache.index_select(0, idx).cpu()
+    width = max(math.ceil(w.k_lens[b] / 256) for b in ids)
+    bt_sub = torch.full((len(ids), width), -1, dtype=torch.int32)
+    for j, b in enumerate(ids):
+        n = math.ceil(w.k_lens[b] / 256)
+        bt_sub[j, :n] = torch.tensor([remap[int(x)] for x in bt[b, :n].tolist()], dtype=torch.int32)
+    slots = w.slot_mapping.cpu()[ids]
+    new_slots = torch.tensor([remap[int(s) // 256] * 256 + int(s) % 256 for s in slots], dtype=torch.int32)
+    q = w.q[: len(ids)].cpu()
+    k = w.k[: len(ids)].cpu()
+    v = w.v[: len(ids)].cpu()
+    cu_q = torch.arange(len(ids) + 1, dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(__import__("itertools").accumulate(w.k_lens[b] for b in ids)), dtype=torch.int32)
+    times = []
+    for _ in range(reps):
+        kc, vc = kc0.clone(), vc0.clone()
+        t0 = time.perf_counter()
+        oracle.store_kvcache(k, v, kc, vc, new_slots)
+        oracle.varlen_attention(q, kc, vc, cu_q, cu_k, SCALE, True, bt_sub)
+        times.append(time.perf_counter() - t0)
+    kv_bytes = sum(w.k_lens[b] * 2 * 2048 for b in ids)
+    med = statistics.median(times)
+    return {"value": round(kv_bytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"CPU oracle (torch fp32, store + paged decode) on the first {len(ids)} of 256 "
+                      f"sequences ({kv_bytes / 1e9:.3f} GB of KV), median of {reps} runs = {med:.3f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configurations")
+    ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU-baseline sample")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the paged-KV path is not sharded across GPUs "
+              f"(asked for --gpus {args.gpus}); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import pagedkv
+    from pagedkv.workloads import make_workload
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("[bench] building cfg2 (256 seqs, Lk ~ U[1024, 8192]) on the GPU")
+    w = make_workload("cfg2", dev)
+    kv_bytes = w.decode_kv_bytes()
+    store_bytes = w.store_bytes()
+    ctx = w.ctx
+    out = torch.empty_like(w.q)
+    pagedkv.reserve_workspace(len(w.q_lens), 16, 128, 1, w.max_seqlen_k, dev)
+
+    def store():
+        pagedkv.store_kvcache(w.k, w.v, w.k_cache, w.v_cache, ctx.slot_mapping)
+
+    def attend():
+        pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                 ctx.max_seqlen_q, ctx.max_seqlen_k, SCALE, True, ctx.block_tables, out=out)
+
+    log(f"[bench] warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        store()
+        attend()
+    torch.cuda.synchronize()
+
+    log(f"[bench] timing {args.steps} steps")
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in evs:
+        store()
+        a.record()
+        attend()
+        b.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    attn_ms = [a.elapsed_time(b) for a, b in evs]
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = kv_bytes / (elapsed / args.steps) / 1e9
+    attn_mean = statistics.fmean(attn_ms)
+    achieved = kv_bytes / (attn_mean * 1e-3) / 1e9
+    log(f"[bench] step {ms_per_step:.3f} ms, decode call {attn_mean:.3f} ms -> {achieved:.1f} GB/s")
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("paged_decode_cfg2_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "paged decode, 256 seqs, Lk~U[1024,8192], 16q/8kv heads, head_dim 128, "
+                        "block 256, shuffled pool; step = store 256 tokens + decode attention",
+            "num_seqs": len(w.q_lens),
+            "kv_bytes_per_step": kv_bytes,
+            "store_bytes_per_step": store_bytes,
+            "num_blocks": int(w.k_cache.shape[0]),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged decode attention call (split-K decode + combine)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "launch_ms_mean": round(attn_mean, 4),
+            "launch_ms_median": round(statistics.median(attn_ms), 4),
+        },
+    }
+
+    if not args.no_extra:
+        result["kernels"] = extra_configs(dev, w)
+    del w
+    torch.cuda.empty_cache()
+
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle on host cores)")
+        wc = make_workload("cfg2", dev)
+        result["cpu_baseline"] = cpu_baseline_decode(wc, args.cpu_seqs)
+        del wc
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def extra_configs(dev, w2):
+    """Per-kernel measurements of the other configurations (events, mean of 20 launches)."""
+    import torch
+
+    import pagedkv
+    from pagedkv.workloads import make_workload
+
+    res = {}
+    # cfg2 store of the 256 new tokens
+    ms, _ = timed_launches(lambda: pagedkv.store_kvcache(w2.k, w2.v, w2.k_cache, w2.v_cache, w2.slot_mapping), 20)
+    res["cfg2_store"] = {"ms": round(ms, 5), "GB/s": round(w2.store_bytes() / ms / 1e6, 1)}
+
+    log("[bench] cfg1")
+    ws = make_workload("cfg1_store", dev)
+    ms, _ = timed_launches(lambda: pagedkv.store_kvcache(ws.k, ws.v, ws.k_cache, ws.v_cache, ws.slot_mapping), 20)
+    res["cfg1_store"] = {"ms": round(ms, 5), "GB/s": round(ws.store_bytes() / ms / 1e6, 1)}
+    wd = make_workload("cfg1_decode", dev)
+    ms, _ = timed_launches(attention_call(wd), 20)
+    res["cfg1_decode"] = {"ms": round(ms, 5), "GB/s": round(wd.decode_kv_bytes() / ms / 1e6, 1)}
+
+    log("[bench] cfg3")
+    w3 = make_workload("cfg3", dev)
+    ms, _ = timed_launches(attention_call(w3), 20)
+    res["cfg3_mixed"] = {"ms": round(ms, 5)}
+    n_dec = sum(1 for lq in w3.q_lens if lq == 1)
+    ms_p, _ = timed_launches(attention_call(w3, sub_batch(w3, lambda i: w3.q_lens[i] > 1)), 20)
+    fl = w3.prefill_flops()
+    res["cfg3_prefill"] = {"ms": round(ms_p, 5), "TFLOP/s": round(fl / ms_p / 1e9, 2),
+                           "mfma_frac": round(fl / ms_p / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4), "flops": fl}
+    ms_d, _ = timed_launches(attention_call(w3, sub_batch(w3, lambda i: w3.q_lens[i] == 1)), 20)
+    kvb = w3.decode_kv_bytes()
+    res["cfg3_decode"] = {"ms": round(ms_d, 5), "GB/s": round(kvb / ms_d / 1e6, 1), "seqs": n_dec}
+
+    log("[bench] cfg4")
+    w4 = make_workload("cfg4", dev)
+    ms, _ = timed_launches(attention_call(w4), 20)
+    res["cfg4_decode"] = {"ms": round(ms, 5), "logical_GB/s": round(w4.decode_kv_bytes() / ms / 1e6, 1),
+                          "unique_GB/s": round(w4.decode_unique_kv_bytes() / ms / 1e6, 1)}
+    return res
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,159 @@
+/*
+ * pagedkv.h -- C-ABI of the MI355X (gfx950) paged-KV attention library
+ * (libpagedkv.so).
+ *
+ * The library implements the device side of the reference's
+ * Attention.forward (src/layers/attention.py:79-105):
+ *
+ *   1. the store_kvcache scatter of new K/V token rows into cache slots
+ *      (src/layers/attention.py:10-34, host wrapper :36-61);
+ *   2. varlen causal attention over either fresh K/V rows ("flat" mode,
+ *      block_table == NULL) or a paged KV cache read through per-sequence
+ *      block tables ("paged" mode) -- the flash_attn_varlen_func call at
+ *      src/layers/attention.py:95-104. Sequences with one query row go to
+ *      the split-K decode kernel, sequences with more go to the bf16-MFMA
+ *      prefill kernel; both run in the same call.
+ *
+ * Conventions
+ *   - Every pointer is a borrowed device pointer; the library allocates
+ *     nothing. Scratch memory for split-K partial results is passed in as
+ *     `workspace` (size from pk_varlen_attention_workspace_bytes).
+ *   - Strides are in ELEMENTS, not bytes.
+ *   - Element type: 16-bit. The store copies bits (bf16 or fp16); the
+ *     attention entry points read and write bf16.
+ *   - Every entry point takes the hipStream_t to enqueue on (0 = the null
+ *     stream), never synchronises, never reads device memory from the host,
+ *     and is safe to record into a hipGraph: all per-sequence lengths are
+ *     read on the device from cu_seqlens_q / cu_seqlens_k.
+ *   - Return value: PK_OK (0) or a negative PK_ERR_* code; the message for
+ *     the last failure on the calling thread is pk_last_error(). Nothing
+ *     throws across the ABI.
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_OK 0
+#define PK_ERR_INVALID_ARG (-1)   /* shape / stride / alignment / null-pointer error */
+#define PK_ERR_UNSUPPORTED (-2)   /* valid but not built (e.g. head_dim != 128)      */
+#define PK_ERR_WORKSPACE (-3)     /* workspace too small or misaligned                 */
+#define PK_ERR_HIP (-4)           /* a HIP runtime call or kernel launch failed        */
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef struct ihipStream_t* pk_stream_t;
+
+/* Version of this ABI (bumped on any signature change). */
+int pk_abi_version(void);
+
+/* Message describing the last error returned on the calling thread
+ * ("" if none). The pointer stays valid until the next call on this thread. */
+const char* pk_last_error(void);
+
+/*
+ * pk_store_kvcache -- replaces store_kvcache() / store_kvcache_kernel
+ * (src/layers/attention.py:36-61 and :10-34).
+ *
+ * For every token i < num_tokens with s = slot_mapping[i] != -1:
+ *     k_cache[s * row_elems + e] = key[i * key_row_stride + e]
+ *     v_cache[s * row_elems + e] = value[i * value_row_stride + e]
+ * for e < row_elems (row_elems = num_kv_heads * head_dim, the reference's
+ * `D`). Tokens with slot -1 (graph padding, model_runner.py:250-251) are
+ * skipped; their cache bits are untouched.
+ *
+ * num_slots > 0 enables a device-side bound check: a slot outside
+ * [-1, num_slots) is not written (the reference performs no check,
+ * attention.py:59). Pass 0 to mirror the reference exactly.
+ *
+ * Requirements: row_elems % 8 == 0; key, value, k_cache, v_cache 16-byte
+ * aligned; key_row_stride and value_row_stride multiples of 8 elements.
+ * The cache rows are contiguous (the reference asserts
+ * k_cache.stride(1) == D, attention.py:53).
+ */
+int pk_store_kvcache(const void* key, int64_t key_row_stride,
+                     const void* value, int64_t value_row_stride,
+                     void* k_cache, void* v_cache,
+                     const int32_t* slot_mapping, int32_t num_tokens,
+                     int32_t row_elems, int64_t num_slots,
+                     pk_stream_t stream);
+
+/*
+ * pk_varlen_attention -- replaces flash_attn_varlen_func(q, k, v,
+ * cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+ * causal, block_table) as called at src/layers/attention.py:95-104.
+ *
+ *   q    (Nq, num_heads, head_dim) bf16, token row stride q_row_stride,
+ *        head stride head_dim (heads contiguous within a row).
+ *   k, v flat mode  (block_table == NULL): (Nk, num_kv_heads, head_dim),
+ *          key row of sequence b, position t at k + (cu_seqlens_k[b] + t) *
+ *          k_row_stride; k_block_stride / v_block_stride are ignored.
+ *        paged mode (block_table != NULL): caches (num_blocks, block_size,
+ *          num_kv_heads, head_dim); position t of sequence b lives at
+ *          k + block_table[b * block_table_stride + t / block_size] *
+ *          k_block_stride + (t % block_size) * k_row_stride.
+ *   cu_seqlens_q, cu_seqlens_k  (num_seqs + 1,) int32 prefix sums.
+ *        Sequence b has Lq = cu_seqlens_q[b+1] - cu_seqlens_q[b] query rows
+ *        and Lk = cu_seqlens_k[b+1] - cu_seqlens_k[b] keys; sequences with
+ *        Lq <= 0 or Lk <= 0 (graph padding, model_runner.py:252-255) are
+ *        skipped and their output rows are not written.
+ *   max_seqlen_q, max_seqlen_k  host-side upper bounds (launch sizes only).
+ *   causal != 0: bottom-right aligned mask -- query row i of a sequence
+ *        sees keys t <= i + Lk - Lq. A row that sees no key is written as 0.
+ *   GQA: query head h reads kv head h / (num_heads / num_kv_heads).
+ *   out  (Nq, num_heads, head_dim) bf16, token row stride out_row_stride.
+ *
+ * Built for head_dim == 128, num_heads % num_kv_heads == 0 with the group
+ * size in {1, 2, 4, 8}; block_size a multiple of 64 in paged mode.
+ * Softmax and accumulation are fp32.
+ */
+int pk_varlen_attention(const void* q, int64_t q_row_stride,
+                        const void* k, const void* v,
+                        int64_t k_row_stride, int64_t v_row_stride,
+                        int64_t k_block_stride, int64_t v_block_stride,
+                        const int32_t* block_table, int32_t block_table_stride,
+                        int32_t block_size,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                        int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        float softmax_scale, int32_t causal,
+                        void* out, int64_t out_row_stride,
+                        void* workspace, size_t workspace_bytes,
+                        pk_stream_t stream);
+
+/*
+ * Bytes of workspace pk_varlen_attention needs for these launch bounds
+ * (the split-K partial outputs of the decode kernel). No counterpart in the
+ * reference: flash-attn allocates its split-K buffers internally, which a
+ * graph-capturable, allocation-free ABI cannot do.
+ */
+size_t pk_varlen_attention_workspace_bytes(int32_t num_seqs, int32_t num_heads,
+                                           int32_t head_dim, int32_t max_seqlen_q,
+                                           int32_t max_seqlen_k);
+
+/*
+ * pk_gather_kv -- materialise the keys (or values) of every sequence from a
+ * paged cache into a flat (sum Lk, row_elems) buffer:
+ *     dst[(cu_seqlens_k[b] + t) * row_elems + e] =
+ *         cache[block_table[b * block_table_stride + t / block_size] *
+ *               block_stride + (t % block_size) * row_elems + e]
+ * This is the block-table addressing flash-attn performs internally for
+ * paged K/V (attention.py:93-104 with model_runner.py:168-172); it has no
+ * separate reference function and exists so the addressing can be checked
+ * bit-exactly and so a paged prefix can be copied out. Same alignment
+ * rules as pk_store_kvcache.
+ */
+int pk_gather_kv(const void* cache, int64_t block_stride, int32_t block_size,
+                 const int32_t* block_table, int32_t block_table_stride,
+                 const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t max_seqlen_k,
+                 int32_t row_elems, void* dst, pk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDKV_H */

@@ -1,0 +1,218 @@
+// extern "C" entry points of libpagedkv.so (declared in include/pagedkv.h).
+//
+// Each entry point validates its arguments on the host (shapes, strides, 16-byte
+// alignment of every vector-loaded pointer), fills the kernel argument block and
+// enqueues on the caller's stream. Nothing here allocates, synchronises or reads
+// device memory, so every call can be recorded into a hipGraph.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/pagedkv.h"
+#include "common.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return PK_OK;
+  return fail(PK_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr size_t kWorkspaceAlign = 256;
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct WorkspaceLayout {
+  int split_tokens;
+  int max_splits;
+  size_t part_o_bytes;
+  size_t part_ml_bytes;
+  size_t total;
+};
+
+WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_k) {
+  WorkspaceLayout w{};
+  w.split_tokens = pk::decode_split_tokens(num_seqs, max_seqlen_k);
+  w.max_splits = max_seqlen_k > 0 ? (max_seqlen_k + w.split_tokens - 1) / w.split_tokens : 0;
+  if (w.max_splits <= 1) return w;  // single-split sequences write their output directly
+  const size_t units = (size_t)num_seqs * (size_t)w.max_splits * (size_t)num_heads;
+  w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
+  w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
+  w.total = w.part_o_bytes + w.part_ml_bytes;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_abi_version(void) { return 1; }
+
+const char* pk_last_error(void) { return g_last_error.c_str(); }
+
+int pk_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                     int64_t value_row_stride, void* k_cache, void* v_cache,
+                     const int32_t* slot_mapping, int32_t num_tokens, int32_t row_elems,
+                     int64_t num_slots, pk_stream_t stream) {
+  g_last_error.clear();
+  if (num_tokens < 0) return fail(PK_ERR_INVALID_ARG, "store_kvcache: num_tokens=%d < 0", num_tokens);
+  if (num_tokens == 0) return PK_OK;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return fail(PK_ERR_INVALID_ARG, "store_kvcache: null pointer argument");
+  if (row_elems <= 0 || row_elems % 8 != 0)
+    return fail(PK_ERR_INVALID_ARG, "store_kvcache: row_elems=%d must be a positive multiple of 8", row_elems);
+  if (key_row_stride < row_elems || value_row_stride < row_elems)
+    return fail(PK_ERR_INVALID_ARG, "store_kvcache: row strides (%lld, %lld) smaller than row_elems=%d",
+                (long long)key_row_stride, (long long)value_row_stride, row_elems);
+  if (key_row_stride % 8 != 0 || value_row_stride % 8 != 0)
+    return fail(PK_ERR_INVALID_ARG, "store_kvcache: row strides (%lld, %lld) must be multiples of 8 elements",
+                (long long)key_row_stride, (long long)value_row_stride);
+  if (!aligned16(key) || !aligned16(value) || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(PK_ERR_INVALID_ARG, "store_kvcache: key/value/cache pointers must be 16-byte aligned");
+  if (num_slots < 0) return fail(PK_ERR_INVALID_ARG, "store_kvcache: num_slots < 0");
+  return hip_status(pk::launch_store_kvcache(key, key_row_stride, value, value_row_stride, k_cache,
+                                             v_cache, slot_mapping, num_tokens, row_elems,
+                                             num_slots, reinterpret_cast<hipStream_t>(stream)),
+                    "store_kvcache launch");
+}
+
+int pk_gather_kv(const void* cache, int64_t block_stride, int32_t block_size,
+                 const int32_t* block_table, int32_t block_table_stride,
+                 const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t max_seqlen_k,
+                 int32_t row_elems, void* dst, pk_stream_t stream) {
+  g_last_error.clear();
+  if (num_seqs < 0 || max_seqlen_k < 0)
+    return fail(PK_ERR_INVALID_ARG, "gather_kv: negative num_seqs or max_seqlen_k");
+  if (num_seqs == 0 || max_seqlen_k == 0) return PK_OK;
+  if (num_seqs > 65535) return fail(PK_ERR_INVALID_ARG, "gather_kv: num_seqs=%d > 65535", num_seqs);
+  if (!cache || !block_table || !cu_seqlens_k || !dst)
+    return fail(PK_ERR_INVALID_ARG, "gather_kv: null pointer argument");
+  if (row_elems <= 0 || row_elems % 8 != 0 || block_stride % 8 != 0 || block_size <= 0 ||
+      block_stride < (int64_t)block_size * row_elems)
+    return fail(PK_ERR_INVALID_ARG, "gather_kv: bad row_elems=%d / block_size=%d / block_stride=%lld",
+                row_elems, block_size, (long long)block_stride);
+  if (!aligned16(cache) || !aligned16(dst))
+    return fail(PK_ERR_INVALID_ARG, "gather_kv: cache and dst must be 16-byte aligned");
+  return hip_status(pk::launch_gather_kv(cache, block_stride, block_size, block_table,
+                                         block_table_stride, cu_seqlens_k, num_seqs, max_seqlen_k,
+                                         row_elems, dst, reinterpret_cast<hipStream_t>(stream)),
+                    "gather_kv launch");
+}
+
+size_t pk_varlen_attention_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                           int32_t max_seqlen_q, int32_t max_seqlen_k) {
+  (void)max_seqlen_q;
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0) return 0;
+  return workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_k).total;
+}
+
+int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, const void* v,
+                        int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                        int64_t v_block_stride, const int32_t* block_table,
+                        int32_t block_table_stride, int32_t block_size,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                        int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+                        int32_t causal, void* out, int64_t out_row_stride, void* workspace,
+                        size_t workspace_bytes, pk_stream_t stream) {
+  g_last_error.clear();
+  if (head_dim != pk::kHeadDim)
+    return fail(PK_ERR_UNSUPPORTED, "varlen_attention: head_dim=%d not built (only %d)", head_dim, pk::kHeadDim);
+  if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: negative num_seqs / max_seqlen");
+  if (num_seqs > 65535) return fail(PK_ERR_INVALID_ARG, "varlen_attention: num_seqs=%d > 65535", num_seqs);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: num_heads=%d not a multiple of num_kv_heads=%d",
+                num_heads, num_kv_heads);
+  const int group = num_heads / num_kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return fail(PK_ERR_UNSUPPORTED, "varlen_attention: GQA group %d not built (1, 2, 4, 8)", group);
+  if (num_seqs == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) return PK_OK;
+  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: q/k/v/out must be 16-byte aligned");
+  const int64_t kv_row = (int64_t)num_kv_heads * head_dim;
+  if (q_row_stride < (int64_t)num_heads * head_dim || out_row_stride < (int64_t)num_heads * head_dim ||
+      k_row_stride < kv_row || v_row_stride < kv_row)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: a row stride is smaller than its row");
+  if (q_row_stride % 8 || out_row_stride % 8 || k_row_stride % 8 || v_row_stride % 8)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: row strides must be multiples of 8 elements");
+  const bool paged = block_table != nullptr;
+  if (paged) {
+    if (block_size <= 0 || block_size % 64 != 0)
+      return fail(PK_ERR_INVALID_ARG, "varlen_attention: block_size=%d must be a positive multiple of 64",
+                  block_size);
+    if (block_table_stride < (max_seqlen_k + block_size - 1) / block_size)
+      return fail(PK_ERR_INVALID_ARG,
+                  "varlen_attention: block_table_stride=%d < ceil(max_seqlen_k=%d / block_size=%d)",
+                  block_table_stride, max_seqlen_k, block_size);
+    if (k_block_stride % 8 || v_block_stride % 8 || k_block_stride < (int64_t)block_size * k_row_stride ||
+        v_block_stride < (int64_t)block_size * v_row_stride)
+      return fail(PK_ERR_INVALID_ARG, "varlen_attention: bad cache block strides (%lld, %lld)",
+                  (long long)k_block_stride, (long long)v_block_stride);
+  }
+  if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: softmax_scale must be positive and finite");
+
+  const WorkspaceLayout ws = workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_k);
+  if (ws.total > 0) {
+    if (!workspace || workspace_bytes < ws.total)
+      return fail(PK_ERR_WORKSPACE, "varlen_attention: workspace of %zu bytes needed, %zu given",
+                  ws.total, workspace ? workspace_bytes : (size_t)0);
+    if ((reinterpret_cast<uintptr_t>(workspace) % kWorkspaceAlign) != 0)
+      return fail(PK_ERR_WORKSPACE, "varlen_attention: workspace must be %zu-byte aligned", kWorkspaceAlign);
+  }
+
+  pk::AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_row_stride = q_row_stride;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.k_row_stride = k_row_stride;
+  a.v_row_stride = v_row_stride;
+  a.k_block_stride = paged ? k_block_stride : 0;
+  a.v_block_stride = paged ? v_block_stride : 0;
+  a.block_table = block_table;
+  a.bt_stride = paged ? block_table_stride : 0;
+  a.block_size = paged ? block_size : 0;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.num_seqs = num_seqs;
+  a.max_seqlen_k = max_seqlen_k;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_row_stride = out_row_stride;
+  a.split_tokens = ws.split_tokens;
+  a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
+  if (ws.total > 0) {
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.part_o_bytes);
+  }
+
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc = hip_status(pk::launch_decode(a, group, paged, max_seqlen_k, s), "decode launch");
+  if (rc != PK_OK) return rc;
+  if (max_seqlen_q > 1)
+    rc = hip_status(pk::launch_prefill(a, group, paged, causal != 0, max_seqlen_q, s), "prefill launch");
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,102 @@
+// Shared definitions for the gfx950 paged-KV kernels (libpagedkv.so).
+//
+// Layout facts every kernel relies on (reference: src/engine/model_runner.py:159-165,
+// src/layers/attention.py:51-53):
+//   * a KV cache is (num_blocks, block_size, num_kv_heads, head_dim), 16-bit elements;
+//     slot s = block * block_size + offset addresses one contiguous token row of
+//     num_kv_heads * head_dim elements;
+//   * q and out are (tokens, num_heads, head_dim) with heads contiguous inside a row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pk {
+
+constexpr int kHeadDim = 128;   // the only head_dim built (Qwen3 family)
+constexpr int kWave = 64;       // CDNA wavefront width
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+// Everything the attention kernels need; passed by value as the kernel argument.
+struct AttnArgs {
+  const uint16_t* q;
+  int64_t q_row_stride;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t k_row_stride, v_row_stride;
+  int64_t k_block_stride, v_block_stride;
+  const int32_t* block_table;   // nullptr in flat mode
+  int32_t bt_stride;
+  int32_t block_size;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int32_t num_seqs;
+  int32_t max_seqlen_k;         // keys past this bound are ignored (keeps every access in bounds)
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  float scale_log2;             // softmax_scale * log2(e): scores live in the exp2 domain
+  uint16_t* out;
+  int64_t out_row_stride;
+  // split-K decode scratch (workspace)
+  float* part_o;                // [num_seqs][max_splits][num_heads][head_dim]
+  float* part_ml;               // [num_seqs][max_splits][num_heads][2] = (max, sum)
+  int32_t split_tokens;
+  int32_t max_splits;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16, round to nearest even (gfx950 converts in hardware).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// DPP lane moves inside a 16-lane row (bound_ctrl: out-of-row sources read 0).
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i inside each half-row
+constexpr int kDppMirror = 0x140;     // lane i <- lane 15-i inside each row
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return v;
+}
+
+__device__ __forceinline__ float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+}  // namespace pk
+
+// Host-side launchers (one per kernel file); each returns a hipError_t.
+namespace pk {
+hipError_t launch_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                                int64_t value_row_stride, void* k_cache, void* v_cache,
+                                const int32_t* slot_mapping, int32_t num_tokens,
+                                int32_t row_elems, int64_t num_slots, hipStream_t stream);
+hipError_t launch_gather_kv(const void* cache, int64_t block_stride, int32_t block_size,
+                            const int32_t* block_table, int32_t bt_stride,
+                            const int32_t* cu_k, int32_t num_seqs, int32_t max_seqlen_k,
+                            int32_t row_elems, void* dst, hipStream_t stream);
+// Split-K decode over sequences with exactly one query row, plus the combine pass.
+hipError_t launch_decode(const AttnArgs& a, int group, bool paged, int max_seqlen_k,
+                         hipStream_t stream);
+// bf16-MFMA attention over sequences with more than one query row.
+hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal,
+                          int max_seqlen_q, hipStream_t stream);
+// Split size (keys per work-group) the decode kernel uses for these launch bounds.
+int decode_split_tokens(int num_seqs, int max_seqlen_k);
+}  // namespace pk

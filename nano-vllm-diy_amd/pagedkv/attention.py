@@ -1,0 +1,58 @@
+"""Drop-in Attention layer for the paged-KV path.
+
+Same class, constructor and forward(q, k, v, ctx) as the reference's Attention
+(src/layers/attention.py:63-105), and the same store_kvcache helper (:36-61), but
+every device operation is a hand-written gfx950 HIP kernel from libpagedkv.so:
+
+* forward stores the new K/V rows into the bound cache first (when the runner has
+  bound one; attention.py:87-88), so a token attends to itself;
+* with ctx.block_tables set it reads K/V from the paged cache, otherwise from the
+  fresh k / v rows (attention.py:93-94);
+* one call covers a mixed batch: one-row sequences go to the split-K decode kernel
+  and longer ones to the MFMA prefill kernel, both bottom-right causal.
+
+The runner rebinds k_cache / v_cache to per-layer views of its KV tensor
+(model_runner.py:159-165), exactly as with the reference layer.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .context import Context
+from .ops import store_kvcache as _store_kvcache
+from .ops import varlen_attention
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Reference signature of store_kvcache (attention.py:36-42)."""
+    _store_kvcache(key, value, k_cache, v_cache, slot_mapping)
+
+
+class Attention(nn.Module):
+    def __init__(self, head_dim: int, num_heads: int, num_kv_heads: int, scale: float = None):
+        super().__init__()
+        self.head_dim = head_dim
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.scale = scale
+        self.k_cache = torch.tensor([])
+        self.v_cache = torch.tensor([])
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ctx: Context) -> torch.Tensor:
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() and v_cache.numel():
+            store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
+        if ctx.block_tables is not None:
+            k, v = k_cache, v_cache
+        return varlen_attention(
+            q, k, v,
+            cu_seqlens_q=ctx.cu_seqlens_q,
+            cu_seqlens_k=ctx.cu_seqlens_k,
+            max_seqlen_q=ctx.max_seqlen_q,
+            max_seqlen_k=ctx.max_seqlen_k,
+            softmax_scale=self.scale,
+            causal=True,
+            block_table=ctx.block_tables,
+        )

@@ -1,0 +1,203 @@
+"""Torch-facing wrappers around the libpagedkv C-ABI.
+
+Each wrapper checks layouts the way the reference does (src/layers/attention.py:
+51-56) plus what the kernels need (bf16, 16-byte aligned rows, int32 metadata on
+the same device), then calls the C entry point on the current torch stream with
+raw device pointers. No wrapper synchronises or reads device memory, so all of
+them can run under torch.cuda.graph capture.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib
+
+_workspaces: dict[int, torch.Tensor] = {}  # device index -> cached workspace
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _req_i32(name: str, t: torch.Tensor, device: torch.device) -> None:
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                  check_slots: bool = False) -> None:
+    """Scatter new K/V token rows into their cache slots.
+
+    Mirrors store_kvcache (src/layers/attention.py:36-61): key/value (N, Hkv, D)
+    with contiguous heads (any token row stride), caches (NB, BS, Hkv, D) with
+    contiguous token rows, slot_mapping (N,) int32 where -1 skips the token.
+    check_slots=True makes the kernel ignore slots outside the cache (the reference
+    has no such check; attention.py:59 is commented out).
+    """
+    batch_seq_len, num_kv_heads, head_dim = key.shape
+    row = num_kv_heads * head_dim
+    # the reference's layout checks (attention.py:51-56)
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == row and v_cache.stride(1) == row
+    assert slot_mapping.numel() == batch_seq_len
+    if value.shape != key.shape:
+        raise ValueError(f"value shape {tuple(value.shape)} != key shape {tuple(key.shape)}")
+    if key.element_size() != 2 or value.dtype != key.dtype or k_cache.dtype != key.dtype or \
+            v_cache.dtype != key.dtype:
+        raise TypeError("key, value and caches must share one 16-bit dtype")
+    if k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim or v_cache.stride(-1) != 1 or \
+            v_cache.stride(-2) != head_dim:
+        raise ValueError("cache rows must be contiguous (heads x head_dim)")
+    dev = key.device
+    for name, t in (("value", value), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    _req_i32("slot_mapping", slot_mapping, dev)
+    if batch_seq_len == 0:
+        return
+    if not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous")
+    num_slots = k_cache.numel() // row if check_slots else 0
+    check(lib().pk_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(),
+        batch_seq_len, row, num_slots, _stream(key)), "pk_store_kvcache")
+
+
+def workspace_bytes(num_seqs: int, num_heads: int, head_dim: int, max_seqlen_q: int,
+                    max_seqlen_k: int) -> int:
+    """Scratch bytes varlen_attention needs for these launch bounds."""
+    return int(lib().pk_varlen_attention_workspace_bytes(
+        num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k))
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    """Per-device scratch, grown outside graph capture and reused afterwards.
+
+    Under capture a too-small cached buffer is not replaced (that would free memory a
+    recorded graph may still use); a private buffer from the capture pool is used.
+    """
+    if nbytes == 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(idx)
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
+    fresh = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if not torch.cuda.is_current_stream_capturing():
+        _workspaces[idx] = fresh
+    return fresh
+
+
+def reserve_workspace(num_seqs: int, num_heads: int, head_dim: int, max_seqlen_q: int,
+                      max_seqlen_k: int, device: torch.device | str = "cuda") -> None:
+    """Grow the cached workspace ahead of graph capture (call outside capture)."""
+    _workspace(workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k),
+               torch.device(device))
+
+
+def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                     max_seqlen_q: int, max_seqlen_k: int,
+                     softmax_scale: float | None = None, causal: bool = True,
+                     block_table: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal varlen attention with optional paged K/V; bf16 in and out.
+
+    Same arguments and meaning as the flash_attn_varlen_func call of the reference
+    (src/layers/attention.py:95-104): q (Nq, Hq, D); k, v flat (Nk, Hkv, D) when
+    block_table is None, else caches (NB, BS, Hkv, D) read through block_table
+    (S, W) int32; per-sequence lengths from cu_seqlens_q / cu_seqlens_k (S + 1,)
+    int32; bottom-right-aligned causal mask; GQA h -> h // (Hq / Hkv).
+    Returns out (Nq, Hq, D) bf16.
+    """
+    nq, num_heads, head_dim = q.shape
+    dev = q.device
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("q, k and v must be bfloat16")
+    if q.stride(-1) != 1 or q.stride(1) != head_dim:
+        raise ValueError("q must have contiguous heads (stride(1) == head_dim, stride(2) == 1)")
+    for name, t in (("k", k), ("v", v), ("cu_seqlens_k", cu_seqlens_k)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    _req_i32("cu_seqlens_q", cu_seqlens_q, dev)
+    _req_i32("cu_seqlens_k", cu_seqlens_k, dev)
+    if not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):
+        raise ValueError("cu_seqlens_q / cu_seqlens_k must be contiguous")
+    num_seqs = cu_seqlens_q.numel() - 1
+    if cu_seqlens_k.numel() != num_seqs + 1:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must have the same length")
+    if block_table is None:
+        if k.dim() != 3 or v.shape != k.shape:
+            raise ValueError("flat mode expects k, v of shape (Nk, Hkv, D)")
+        num_kv_heads = k.shape[1]
+        k_row, v_row, k_blk, v_blk = k.stride(0), v.stride(0), 0, 0
+        bt_ptr, bt_stride, block_size = 0, 0, 0
+        kv_inner = (k.stride(1), k.stride(2), v.stride(1), v.stride(2))
+    else:
+        if k.dim() != 4 or v.shape != k.shape:
+            raise ValueError("paged mode expects caches of shape (NB, BS, Hkv, D)")
+        _req_i32("block_table", block_table, dev)
+        if block_table.dim() != 2 or block_table.stride(1) != 1:
+            raise ValueError("block_table must be (S, W) with contiguous rows")
+        if block_table.shape[0] < num_seqs:
+            raise ValueError("block_table has fewer rows than sequences")
+        num_kv_heads = k.shape[2]
+        block_size = k.shape[1]
+        k_row, v_row, k_blk, v_blk = k.stride(1), v.stride(1), k.stride(0), v.stride(0)
+        bt_ptr, bt_stride = block_table.data_ptr(), block_table.stride(0)
+        kv_inner = (k.stride(2), k.stride(3), v.stride(2), v.stride(3))
+    if k.shape[-1] != head_dim:
+        raise ValueError(f"k head_dim {k.shape[-1]} != q head_dim {head_dim}")
+    if kv_inner != (head_dim, 1, head_dim, 1):
+        raise ValueError("k and v must have contiguous heads within a token row")
+    if out is None:
+        out = torch.empty(nq, num_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    elif out.shape != q.shape or out.dtype != torch.bfloat16 or out.stride(-1) != 1 or \
+            out.stride(1) != head_dim:
+        raise ValueError("out must be (Nq, Hq, D) bf16 with contiguous heads")
+    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    nbytes = workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k)
+    ws = _workspace(nbytes, dev)
+    check(lib().pk_varlen_attention(
+        q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(),
+        k_row, v_row, k_blk, v_blk,
+        bt_ptr, bt_stride, block_size,
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+        num_seqs, int(max_seqlen_q), int(max_seqlen_k),
+        num_heads, num_kv_heads, head_dim,
+        scale, 1 if causal else 0,
+        out.data_ptr(), out.stride(0),
+        ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
+        _stream(q)), "pk_varlen_attention")
+    return out
+
+
+def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_k: torch.Tensor,
+              max_seqlen_k: int, total_k: int | None = None) -> torch.Tensor:
+    """Flat (sum Lk, Hkv, D) copy of each sequence's cache rows via its block table.
+
+    total_k (= cu_seqlens_k[-1]) sizes the output; pass it to avoid a device read.
+    """
+    dev = cache.device
+    _req_i32("block_table", block_table, dev)
+    _req_i32("cu_seqlens_k", cu_seqlens_k, dev)
+    if cache.dim() != 4 or cache.stride(-1) != 1 or cache.stride(-2) != cache.shape[-1] or \
+            cache.stride(1) != cache.shape[-1] * cache.shape[-2]:
+        raise ValueError("cache must be (NB, BS, Hkv, D) with contiguous token rows")
+    if block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be (S, W) with contiguous rows")
+    num_seqs = cu_seqlens_k.numel() - 1
+    if total_k is None:
+        total_k = int(cu_seqlens_k[-1].item())
+    row = cache.shape[2] * cache.shape[3]
+    dst = torch.empty(total_k, cache.shape[2], cache.shape[3], dtype=cache.dtype, device=dev)
+    check(lib().pk_gather_kv(
+        cache.data_ptr(), cache.stride(0), cache.shape[1], block_table.data_ptr(),
+        block_table.stride(0), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_k), row,
+        dst.data_ptr(), _stream(cache)), "pk_gather_kv")
+    return dst
