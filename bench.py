@@ -58,50 +58,35 @@ def timed_launches(fn, reps: int, warmup: int = 3):
 
 
 def attention_call(w, sub=None):
-    """Closure running the path's attention op on workload w (optionally a sub-batch)."""
+    """Closure running the path's attention op on workload w, or on a sub-batch of it."""
     import pagedkv
 
-    cu_q, cu_k, bt, mq, mk = w.cu_seqlens_q, w.cu_seqlens_k, w.block_tables, w.max_seqlen_q, w.max_seqlen_k
-    if sub is not None:
-        cu_q, cu_k, bt, mq, mk = sub
-    out = pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt)
+    q, cu_q, cu_k, bt, mq, mk = (w.q, w.cu_seqlens_q, w.cu_seqlens_k, w.block_tables,
+                                 w.max_seqlen_q, w.max_seqlen_k) if sub is None else sub
+    out = pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt)
 
     def fn():
-        pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt, out=out)
+        pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt, out=out)
     return fn
 
 
 def sub_batch(w, keep):
-    """Metadata selecting only sequences `keep` (others padded to length 0)."""
+    """(q, cu_seqlens_q, cu_seqlens_k, block_tables, max_q, max_k) of the sequences i with keep(i)."""
+    import itertools
+
     import torch
 
-    q_lens = [lq if keep(i) else 0 for i, lq in enumerate(w.q_lens)]
-    k_lens = [lk if keep(i) else 0 for i, lk in enumerate(w.k_lens)]
-    # rows keep their positions in q: express skipped sequences as zero-length spans
-    cu_q, cu_k, a, c = [0], [0], 0, 0
-    for i, (lq, lk) in enumerate(zip(w.q_lens, w.k_lens)):
-        a += lq
-        c += lk
-        cu_q.append(a)
-        cu_k.append(c)
-    # a skipped sequence gets Lq = 0 by repeating the previous offset
-    cq, ck = [0], [0]
-    for i in range(len(w.q_lens)):
-        cq.append(cu_q[i + 1] if keep(i) else cu_q[i])
-        ck.append(ck[-1] + k_lens[i])
-        if not keep(i):
-            cq[-1] = cq[-2]
-    # q rows are addressed by cu_q[b]; skipped sequences have Lq = 0 so are never read,
-    # but kept sequences must still start at their own rows
-    cq = [0] + [cu_q[i + 1] if keep(i) else cu_q[i] for i in range(len(w.q_lens))]
-    starts = [cu_q[i] for i in range(len(w.q_lens))]
+    ids = [i for i in range(len(w.q_lens)) if keep(i)]
+    cu_q = w.cu_seqlens_q.cpu().tolist()
+    rows = [r for i in ids for r in range(cu_q[i], cu_q[i + 1])]
     dev = w.q.device
-    # Build explicit start/end pairs: Lq_b = cq[b+1] - cq[b] must be the kept length and
-    # cq[b] must equal the sequence's first row. Use per-sequence (start, start + Lq).
-    ok = all(cq[i] == starts[i] or not keep(i) for i in range(len(starts)))
-    assert ok
-    return (torch.tensor(cq, dtype=torch.int32, device=dev), torch.tensor(ck, dtype=torch.int32, device=dev),
-            w.block_tables, max(q_lens), max(k_lens))
+    q = w.q.index_select(0, torch.tensor(rows, dtype=torch.long, device=dev))
+    lq = [w.q_lens[i] for i in ids]
+    lk = [w.k_lens[i] for i in ids]
+    cq = torch.tensor([0, *itertools.accumulate(lq)], dtype=torch.int32, device=dev)
+    ck = torch.tensor([0, *itertools.accumulate(lk)], dtype=torch.int32, device=dev)
+    bt = w.block_tables.index_select(0, torch.tensor(ids, dtype=torch.long, device=dev)).contiguous()
+    return q, cq, ck, bt, max(lq), max(lk)
 
 
 def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
@@ -109,8 +94,6 @@ def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
     import torch
 
     import oracle  # CPU baseline leg only
-    sys.path.insert(0, str(ROOT / "tests"))
-    from paged_helpers import subset_oracle  # noqa: F401  (shares the block-subsetting logic)
 
     torch.set_num_threads(os.cpu_count() or 1)
     ids = list(range(min(max_seqs, len(w.q_lens))))

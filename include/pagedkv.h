@@ -17,7 +17,9 @@
  * Conventions
  *   - Every pointer is a borrowed device pointer; the library allocates
  *     nothing. Scratch memory for split-K partial results is passed in as
- *     `workspace` (size from pk_varlen_attention_workspace_bytes).
+ *     `workspace` (size from pk_varlen_attention_workspace_bytes; no
+ *     initial contents needed). Two calls that can run at the same time
+ *     (e.g. on different streams) must not share a workspace.
  *   - Strides are in ELEMENTS, not bytes.
  *   - Element type: 16-bit. The store copies bits (bf16 or fp16); the
  *     attention entry points read and write bf16.
@@ -126,10 +128,11 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride,
                         pk_stream_t stream);
 
 /*
- * Bytes of workspace pk_varlen_attention needs for these launch bounds
- * (the split-K partial outputs of the decode kernel). No counterpart in the
- * reference: flash-attn allocates its split-K buffers internally, which a
- * graph-capturable, allocation-free ABI cannot do.
+ * Bytes of workspace pk_varlen_attention needs for these launch bounds (the
+ * split-K partial outputs of the decode kernel; 0 when every sequence fits
+ * one split, in which case workspace may be NULL). No
+ * counterpart in the reference: flash-attn allocates its split-K buffers
+ * internally, which a graph-capturable, allocation-free ABI cannot do.
  */
 size_t pk_varlen_attention_workspace_bytes(int32_t num_seqs, int32_t num_heads,
                                            int32_t head_dim, int32_t max_seqlen_q,

@@ -34,6 +34,7 @@ int hip_status(hipError_t err, const char* what) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr size_t kWorkspaceAlign = 256;
+constexpr int kMaxSeqs = 65535;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -45,14 +46,17 @@ struct WorkspaceLayout {
   size_t total;
 };
 
+// [per-split partial numerators | per-split (max, sum)]; empty when no sequence can
+// have more than one split (those write their output directly).
 WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_k) {
   WorkspaceLayout w{};
   w.split_tokens = pk::decode_split_tokens(num_seqs, max_seqlen_k);
   w.max_splits = max_seqlen_k > 0 ? (max_seqlen_k + w.split_tokens - 1) / w.split_tokens : 0;
-  if (w.max_splits <= 1) return w;  // single-split sequences write their output directly
-  const size_t units = (size_t)num_seqs * (size_t)w.max_splits * (size_t)num_heads;
-  w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
-  w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
+  if (w.max_splits > 1) {  // single-split sequences write their output directly
+    const size_t units = (size_t)num_seqs * (size_t)w.max_splits * (size_t)num_heads;
+    w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
+    w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
+  }
   w.total = w.part_o_bytes + w.part_ml_bytes;
   return w;
 }
@@ -135,7 +139,7 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: head_dim=%d not built (only %d)", head_dim, pk::kHeadDim);
   if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: negative num_seqs / max_seqlen");
-  if (num_seqs > 65535) return fail(PK_ERR_INVALID_ARG, "varlen_attention: num_seqs=%d > 65535", num_seqs);
+  if (num_seqs > kMaxSeqs) return fail(PK_ERR_INVALID_ARG, "varlen_attention: num_seqs=%d > %d", num_seqs, kMaxSeqs);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: num_heads=%d not a multiple of num_kv_heads=%d",
                 num_heads, num_kv_heads);
@@ -153,6 +157,8 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: a row stride is smaller than its row");
   if (q_row_stride % 8 || out_row_stride % 8 || k_row_stride % 8 || v_row_stride % 8)
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: row strides must be multiples of 8 elements");
+  if (k_row_stride >= (1 << 22) || v_row_stride >= (1 << 22))
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention: K/V row strides must be below 2^22 elements");
   const bool paged = block_table != nullptr;
   if (paged) {
     if (block_size <= 0 || block_size % 64 != 0)

@@ -7,40 +7,187 @@
 // over all Lk keys (a single bottom-right-aligned causal row sees every key).
 //
 // Work decomposition
-//   grid = (split, sequence, kv-head group of up to 8); one work-group per (sequence,
-//   split of `split_tokens` keys); wavefront w of the group owns kv head g and both
-//   (all G) query heads that read it, so every K/V row fetched from HBM serves the
-//   whole GQA group. The 8 wavefronts of a group together read whole 2 KiB token rows.
+//   grid = (split, sequence, group of kv heads); a work-group handles one split of
+//   `split_tokens` keys of one sequence for up to 16 kv heads (4 per wavefront), and every
+//   K/V row it reads serves all G query heads of its kv head (GQA reuse in registers).
+//   Sequences with one split write their output directly; longer ones leave per-split
+//   (max, sum, numerator) partials in the workspace that a small combine kernel merges.
 //
-// Lane layout inside a wavefront: lane = 16 * r + c. Lanes of DPP row r hold key
-// row (t + 4u + r) for unrolled step u; lane c holds head_dim elements [8c, 8c+8).
-//   * q.k: 8 FMAs per head per lane, then a 4-step DPP sum across the 16-lane row;
-//     every lane of the row ends with the full score of its key, so the softmax
-//     weight p needed for P.V is already in the lane that holds that key's V chunk.
-//   * running max: one xor-16/xor-32 exchange per step of 4U keys.
-//   * acc[h][8 elements] += p * v is lane-local; the 4 rows are summed once per split.
-// Partial (max, sum, acc) per (sequence, split, head) go to the workspace and a small
-// combine kernel merges them; a sequence with one split writes its output directly.
+// Lane layout: lane = 16 hr + c. DPP row hr holds kv head 4 w + hr of wavefront w and
+// lane c holds head_dim elements [8c, 8c + 8). One dwordx4 load instruction therefore
+// reads one key's 4 heads = 1 KiB of a contiguous cache row (the two wavefronts of an
+// 8-kv-head group read the whole 2 KiB row), the friendliest pattern for HBM.
+//   * q.k: 4 v_dot2_f32_bf16 per (key, query head) on bf16 pairs, then a 4-step DPP sum
+//     across the 16-lane row; every lane of the row ends with the key's full score.
+//   * softmax: keys of a step are lane-local, so the running max needs no shuffles.
+//   * P.V: p rounded to bf16 and paired across two keys, one dot2 per (head, element).
+// Loads are software-pipelined two steps deep and all issued before the step's math.
 #include "common.h"
 
 namespace pk {
 namespace {
 
-constexpr int kDecodeMaxWaves = 8;
+// Build-time tunables (defaults are the measured best on MI355X).
+#ifndef PK_DECODE_WAVES
+#define PK_DECODE_WAVES 4       // max wavefronts (4 kv heads each) per work-group
+#endif
+#ifndef PK_DECODE_STEP_G2
+#define PK_DECODE_STEP_G2 8     // keys per pipeline step for GQA groups <= 2
+#endif
+#ifndef PK_DECODE_SPLIT_MAX
+#define PK_DECODE_SPLIT_MAX 512 // keys per work unit (split) when the batch is large
+#endif
+#ifndef PK_DECODE_NT_FROM
+// Keys at positions >= PK_DECODE_NT_FROM are read with non-temporal (streaming) loads,
+// earlier ones with normal loads. Prefix caching can only share a sequence's leading
+// blocks, so those are the reads worth keeping in L2 / Infinity Cache; everything past
+// them is read once per step and only displaces useful lines. -1 disables streaming loads.
+#define PK_DECODE_NT_FROM 2048
+#endif
+
+constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
+
+__device__ __forceinline__ uint4 load16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ uint4 load16_stream(const char* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(w.x, w.y, w.z, w.w);
+}
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// a.x * b.x + a.y * b.y + c on packed bf16 pairs, fp32 accumulate (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+// Per-lane softmax state of one work unit.
+template <int G>
+struct DecodeState {
+  uint32_t qp[G][4];  // q in bf16 pairs (this lane's 8 elements of each query head)
+  float m[G];         // running max of the unscaled scores
+  float l[G];         // running softmax denominator
+  float acc[G][8];    // running P.V numerator (this lane's 8 elements)
+};
+
+// Issue the K then V loads of keys [t, t + U) of this lane's kv head. lane_bytes is the
+// lane's byte offset inside a token row. Keys past t_end re-read the step's last valid
+// row (same cache block, finite data) and consume() masks them to p = 0, so no load
+// needs a branch and all offsets past the wave-uniform base are the same per lane.
+template <int U, bool PAGED>
+__device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_bytes, int b, int k0, int t,
+                                            int t_end, uint4 (&kr)[U], uint4 (&vr)[U]) {
+  const uint16_t* kp;
+  const uint16_t* vp;
+  if constexpr (PAGED) {
+    // [t, t + U) lies inside one cache block: U divides block_size and split_tokens.
+    const int blk = a.block_table[(int64_t)b * a.bt_stride + t / a.block_size];
+    const int off = t % a.block_size;
+    kp = a.k + (int64_t)blk * a.k_block_stride + (int64_t)off * a.k_row_stride;
+    vp = a.v + (int64_t)blk * a.v_block_stride + (int64_t)off * a.v_row_stride;
+  } else {
+    kp = a.k + (int64_t)(k0 + t) * a.k_row_stride;
+    vp = a.v + (int64_t)(k0 + t) * a.v_row_stride;
+  }
+  const int last = t_end - 1 - t;
+  const bool stream = PK_DECODE_NT_FROM >= 0 && t >= PK_DECODE_NT_FROM;  // wave-uniform
+  if (stream) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      kr[u] = load16_stream(reinterpret_cast<const char*>(kp + (int64_t)min(u, last) * a.k_row_stride) + lane_bytes);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      vr[u] = load16_stream(reinterpret_cast<const char*>(vp + (int64_t)min(u, last) * a.v_row_stride) + lane_bytes);
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      kr[u] = load16(reinterpret_cast<const char*>(kp + (int64_t)min(u, last) * a.k_row_stride) + lane_bytes);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      vr[u] = load16(reinterpret_cast<const char*>(vp + (int64_t)min(u, last) * a.v_row_stride) + lane_bytes);
+  }
+}
+
+// Fold keys [t, t + U) (already loaded) into the running softmax state.
+template <int G, int U>
+__device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int t_end, const uint4 (&kr)[U],
+                                        const uint4 (&vr)[U]) {
+  // unscaled scores: 4 dot2 per (key, head) over this lane's 8 elements, then the
+  // 16-lane DPP sum gives every lane of the row the full q.k of its key.
+  float s[U][G];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      float d0 = dot2(st.qp[i][0], kr[u].x, 0.f);
+      d0 = dot2(st.qp[i][1], kr[u].y, d0);
+      d0 = dot2(st.qp[i][2], kr[u].z, d0);
+      d0 = dot2(st.qp[i][3], kr[u].w, d0);
+      s[u][i] = row16_sum(d0);
+    }
+    if (t + u >= t_end) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) s[u][i] = -INFINITY;
+    }
+  }
+
+  // online softmax in the exp2 domain; p is rounded to bf16 for the P.V dot2 (the
+  // same rounding a bf16 P.V matrix product applies), l sums the fp32 p.
+  uint32_t pk[U / 2][G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    float mx = s[0][i];
+#pragma unroll
+    for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][i]);
+    const float m_new = fmaxf(st.m[i], mx);  // finite: the step holds >= 1 valid key
+    const float alpha = exp2_fast((st.m[i] - m_new) * c2);
+    st.m[i] = m_new;
+    const float ms = m_new * c2;
+    st.l[i] *= alpha;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st.acc[i][e] *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; u += 2) {
+      const float p0 = exp2_fast(fmaf(s[u][i], c2, -ms));
+      const float p1 = exp2_fast(fmaf(s[u + 1][i], c2, -ms));
+      st.l[i] += p0 + p1;
+      pk[u / 2][i] = pack_bf16x2(p0, p1);
+    }
+  }
+
+  // P.V on key pairs (u, u+1): v_perm builds (v_u[e], v_u+1[e]) bf16 pairs shared by
+  // the G heads, one dot2 per (head, element) adds both keys.
+#pragma unroll
+  for (int u = 0; u < U; u += 2) {
+    const uint32_t va[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+    const uint32_t vb[4] = {vr[u + 1].x, vr[u + 1].y, vr[u + 1].z, vr[u + 1].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = __builtin_amdgcn_perm(vb[j], va[j], 0x05040100u);  // elements 2j
+      const uint32_t hi = __builtin_amdgcn_perm(vb[j], va[j], 0x07060302u);  // elements 2j+1
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        st.acc[i][2 * j] = dot2(pk[u / 2][i], lo, st.acc[i][2 * j]);
+        st.acc[i][2 * j + 1] = dot2(pk[u / 2][i], hi, st.acc[i][2 * j + 1]);
+      }
+    }
+  }
+}
+
 template <int G, int U, bool PAGED>
 __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
+  static_assert(U % 2 == 0, "P.V pairs keys");
   constexpr int D = kHeadDim;
-  constexpr int STEP = 4 * U;  // keys per inner step of one wavefront
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int waves = blockDim.x / kWave;
-  const int g = blockIdx.z * waves + wave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
+  // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
+  const int g_first = (blockIdx.z * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
   const int b = blockIdx.y;
   const int split = blockIdx.x;
-  if (g >= a.num_kv_heads) return;
   const int q0 = a.cu_q[b];
   if (a.cu_q[b + 1] - q0 != 1) return;  // rows with Lq != 1 belong to the prefill kernel
   const int k0 = a.cu_k[b];
@@ -50,143 +197,77 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   const int t_end = min(Lk, t_begin + a.split_tokens);
   const int nsplit = (Lk + a.split_tokens - 1) / a.split_tokens;
 
-  const int r = lane >> 4;  // key sub-row 0..3
-  const int c = lane & 15;  // head_dim chunk
+  const int c = lane & 15;
+  const int g_lane = g_first + (lane >> 4);               // this DPP row's kv head
+  const bool row_live = g_lane < a.num_kv_heads;
+  const int g = row_live ? g_lane : a.num_kv_heads - 1;   // idle rows read a valid head
   const int H = a.num_heads;
+  const float c2 = a.scale_log2;
+  const uint32_t lane_bytes = (uint32_t)(g * D + c * 8) * 2u;
 
-  float qf[G][8];
+  // q stays in bf16 pairs: q.k runs on v_dot2_f32_bf16 and the scale is applied to the
+  // fp32 dot product (scores are kept unscaled; c2 enters the exponent).
+  DecodeState<G> st;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + (g * G + i) * D + c * 8);
+    st.qp[i][0] = w.x;
+    st.qp[i][1] = w.y;
+    st.qp[i][2] = w.z;
+    st.qp[i][3] = w.w;
+    st.m[i] = -INFINITY;
+    st.l[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st.acc[i][e] = 0.f;
+  }
+
+  // Two-stage software pipeline: the loads of step n+1 are in flight while step n is
+  // consumed. The prefetch is unconditional (past t_end it re-reads the current step,
+  // which hits in cache) so the wait counts stay exact. The scheduling barriers keep
+  // each step's loads together ahead of its math: otherwise the scheduler sinks every
+  // load next to its first use to save registers, which serialises their latency.
+  uint4 kA[U], vA[U], kB[U], vB[U];
+  issue_loads<U, PAGED>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
+  for (int t = t_begin; t < t_end; t += 2 * U) {
+    const int t1 = t + U;
+    issue_loads<U, PAGED>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    consume<G, U>(st, c2, t, t_end, kA, vA);
+    if (t1 >= t_end) break;
+    const int t2 = t1 + U;
+    issue_loads<U, PAGED>(a, lane_bytes, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    consume<G, U>(st, c2, t1, t_end, kB, vB);
+  }
+
+  if (!row_live) return;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int h = g * G + i;
-    const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + h * D + c * 8);
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qf[i][2 * e] = bf16_lo(ww[e]) * a.scale_log2;
-      qf[i][2 * e + 1] = bf16_hi(ww[e]) * a.scale_log2;
-    }
-  }
-
-  float m[G], l[G], acc[G][8];
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
-  }
-
-  for (int t = t_begin; t < t_end; t += STEP) {
-    // [t, t + STEP) lies inside one cache block: STEP divides block_size and split_tokens.
-    const uint16_t* kp;
-    const uint16_t* vp;
-    if constexpr (PAGED) {
-      const int blk = a.block_table[(int64_t)b * a.bt_stride + t / a.block_size];
-      const int off = t % a.block_size;
-      kp = a.k + (int64_t)blk * a.k_block_stride + (int64_t)off * a.k_row_stride;
-      vp = a.v + (int64_t)blk * a.v_block_stride + (int64_t)off * a.v_row_stride;
-    } else {
-      kp = a.k + (int64_t)(k0 + t) * a.k_row_stride;
-      vp = a.v + (int64_t)(k0 + t) * a.v_row_stride;
-    }
-    kp += g * D + c * 8;
-    vp += g * D + c * 8;
-
-    uint4 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = 4 * u + r;
-      if (t + j < t_end) {
-        kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)j * a.k_row_stride);
-        vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)j * a.v_row_stride);
-      } else {
-        kr[u] = make_uint4(0, 0, 0, 0);  // keys past Lk: score masked, value zero (no NaN * 0)
-        vr[u] = make_uint4(0, 0, 0, 0);
-      }
-    }
-
-    float s[U][G];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t kw[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-#pragma unroll
-      for (int i = 0; i < G; ++i) {
-        float d0 = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          d0 = fmaf(qf[i][2 * e], bf16_lo(kw[e]), d0);
-          d0 = fmaf(qf[i][2 * e + 1], bf16_hi(kw[e]), d0);
-        }
-        s[u][i] = row16_sum(d0);
-      }
-      if (t + 4 * u + r >= t_end) {
-#pragma unroll
-        for (int i = 0; i < G; ++i) s[u][i] = -INFINITY;
-      }
-    }
-
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      float mx = s[0][i];
-#pragma unroll
-      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][i]);
-      mx = fmaxf(mx, xor_shfl(mx, 16));
-      mx = fmaxf(mx, xor_shfl(mx, 32));
-      const float m_new = fmaxf(m[i], mx);  // finite: the step holds >= 1 valid key
-      const float alpha = exp2_fast(m[i] - m_new);
-      m[i] = m_new;
-      l[i] *= alpha;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[i][e] *= alpha;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float p = exp2_fast(s[u][i] - m_new);
-        l[i] += p;
-        const uint32_t vw[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[i][2 * e] = fmaf(p, bf16_lo(vw[e]), acc[i][2 * e]);
-          acc[i][2 * e + 1] = fmaf(p, bf16_hi(vw[e]), acc[i][2 * e + 1]);
-        }
-      }
-    }
-  }
-
-  // Sum the four key sub-rows (lanes c, c+16, c+32, c+48).
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    l[i] += xor_shfl(l[i], 16);
-    l[i] += xor_shfl(l[i], 32);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      acc[i][e] += xor_shfl(acc[i][e], 16);
-      acc[i][e] += xor_shfl(acc[i][e], 32);
-    }
-  }
-
-  if (r != 0) return;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const int h = g * G + i;
-    if (nsplit == 1) {
-      const float inv = 1.f / l[i];
+    if (nsplit == 1) {  // the only split of this sequence: normalise and store
+      const float inv = 1.f / st.l[i];
       uint4 w;
-      w.x = pack_bf16x2(acc[i][0] * inv, acc[i][1] * inv);
-      w.y = pack_bf16x2(acc[i][2] * inv, acc[i][3] * inv);
-      w.z = pack_bf16x2(acc[i][4] * inv, acc[i][5] * inv);
-      w.w = pack_bf16x2(acc[i][6] * inv, acc[i][7] * inv);
+      w.x = pack_bf16x2(st.acc[i][0] * inv, st.acc[i][1] * inv);
+      w.y = pack_bf16x2(st.acc[i][2] * inv, st.acc[i][3] * inv);
+      w.z = pack_bf16x2(st.acc[i][4] * inv, st.acc[i][5] * inv);
+      w.w = pack_bf16x2(st.acc[i][6] * inv, st.acc[i][7] * inv);
       *reinterpret_cast<uint4*>(a.out + (int64_t)q0 * a.out_row_stride + h * D + c * 8) = w;
     } else {
       const int64_t unit = ((int64_t)b * a.max_splits + split) * H + h;
       float4* po = reinterpret_cast<float4*>(a.part_o + unit * D + c * 8);
-      po[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-      po[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
-      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + unit * 2) = make_float2(m[i], l[i]);
+      po[0] = make_float4(st.acc[i][0], st.acc[i][1], st.acc[i][2], st.acc[i][3]);
+      po[1] = make_float4(st.acc[i][4], st.acc[i][5], st.acc[i][6], st.acc[i][7]);
+      // merged in the exp2 domain: store the scaled max
+      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + unit * 2) = make_float2(st.m[i] * c2, st.l[i]);
     }
   }
 }
 
-// Merge the per-split partials of one (sequence, head): thread d owns element d.
+// Merge the per-split partials of one (sequence, head): thread d owns element d. A
+// separate launch (rather than a "last work-group merges" tail in the split kernel) because
+// the XCD L2 caches are not coherent with each other: a device-scope fence per
+// work-group would write back and invalidate a whole L2, while the kernel boundary makes
+// every partial visible for free.
 __global__ __launch_bounds__(kHeadDim) void decode_combine_kernel(const AttnArgs a) {
   constexpr int D = kHeadDim;
   const int h = blockIdx.x;
@@ -213,7 +294,13 @@ __global__ __launch_bounds__(kHeadDim) void decode_combine_kernel(const AttnArgs
 }
 
 template <int G, int U>
-hipError_t launch_decode_g(const AttnArgs& a, bool paged, dim3 grid, dim3 block, hipStream_t stream) {
+hipError_t launch_decode_g(const AttnArgs& a, bool paged, hipStream_t stream) {
+  const int quads = (a.num_kv_heads + 3) / 4;   // wavefronts needed for all kv heads
+  int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
+  while (quads % waves != 0) --waves;            // no idle wavefront in any work-group
+  const int zgroups = quads / waves;
+  const dim3 grid((unsigned)a.max_splits, (unsigned)a.num_seqs, (unsigned)zgroups);
+  const dim3 block((unsigned)(waves * kWave));
   if (paged)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true>), grid, block, 0, stream, a);
   else
@@ -226,7 +313,7 @@ hipError_t launch_decode_g(const AttnArgs& a, bool paged, dim3 grid, dim3 block,
 int decode_split_tokens(int num_seqs, int max_seqlen_k) {
   // One 256-key cache block per work-group when the batch yields enough work-groups
   // to cover the 256 CUs several times; shorter splits for small batches.
-  int split = 256;
+  int split = PK_DECODE_SPLIT_MAX;
   while (split > 64 && (int64_t)num_seqs * ((max_seqlen_k + split - 1) / split) < 2048) split /= 2;
   return split;
 }
@@ -234,16 +321,12 @@ int decode_split_tokens(int num_seqs, int max_seqlen_k) {
 hipError_t launch_decode(const AttnArgs& a, int group, bool paged, int max_seqlen_k,
                          hipStream_t stream) {
   if (a.num_seqs <= 0 || max_seqlen_k <= 0) return hipSuccess;
-  const int waves = a.num_kv_heads < kDecodeMaxWaves ? a.num_kv_heads : kDecodeMaxWaves;
-  const int zgroups = (a.num_kv_heads + waves - 1) / waves;
-  const dim3 grid((unsigned)a.max_splits, (unsigned)a.num_seqs, (unsigned)zgroups);
-  const dim3 block((unsigned)(waves * kWave));
   hipError_t err;
   switch (group) {
-    case 1: err = launch_decode_g<1, 8>(a, paged, grid, block, stream); break;
-    case 2: err = launch_decode_g<2, 8>(a, paged, grid, block, stream); break;
-    case 4: err = launch_decode_g<4, 4>(a, paged, grid, block, stream); break;
-    case 8: err = launch_decode_g<8, 2>(a, paged, grid, block, stream); break;
+    case 1: err = launch_decode_g<1, PK_DECODE_STEP_G2>(a, paged, stream); break;
+    case 2: err = launch_decode_g<2, PK_DECODE_STEP_G2>(a, paged, stream); break;
+    case 4: err = launch_decode_g<4, 4>(a, paged, stream); break;
+    case 8: err = launch_decode_g<8, 4>(a, paged, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;

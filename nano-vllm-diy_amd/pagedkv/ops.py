@@ -79,7 +79,8 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
     """Per-device scratch, grown outside graph capture and reused afterwards.
 
     Under capture a too-small cached buffer is not replaced (that would free memory a
-    recorded graph may still use); a private buffer from the capture pool is used.
+    recorded graph may still use); a private buffer from the capture pool is used. Calls
+    on different streams of one device must not overlap while they share this buffer.
     """
     if nbytes == 0:
         return None

@@ -319,3 +319,25 @@ def test_graph_capture_padded_decode_replay(gpu):
         assert_close_bf16(out_static[:bs], eager.float(), f"replay {rep}")
     # padded rows store nothing: only the real slots (rewritten with identical bits) changed
     assert bits_equal(w.k_cache, cache_before[0]) and bits_equal(w.v_cache, cache_before[1])
+
+
+def test_workspace_reuse_across_batch_shapes(gpu):
+    """One cached workspace serves calls of different shapes in any order: each result is
+    bit-identical to the same call on a fresh (zero-filled) workspace."""
+    import pagedkv.ops as ops
+    shapes = [("cfg4", 16), ("cfg2", 24), ("cfg3", None), ("cfg1_decode", None), ("cfg2", 8), ("cfg3", 40)]
+    wls = [make_workload(n, gpu, num_seqs=s) for n, s in shapes]
+
+    def run(w):
+        return pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k,
+                                        w.max_seqlen_q, w.max_seqlen_k, None, True, w.block_tables)
+    fresh = []
+    for w in wls:
+        ops._workspaces.clear()
+        fresh.append(run(w))
+    ops._workspaces.clear()
+    for rep in range(2):
+        for w, want in zip(wls, fresh):
+            got = run(w)
+            torch.cuda.synchronize()
+            assert bits_equal(got, want), f"{w.name} rep {rep}"
