@@ -41,7 +41,8 @@ namespace {
 // Keys at positions >= PK_DECODE_NT_FROM are read with non-temporal (streaming) loads,
 // earlier ones with normal loads. Prefix caching can only share a sequence's leading
 // blocks, so those are the reads worth keeping in L2 / Infinity Cache; everything past
-// them is read once per step and only displaces useful lines. -1 disables streaming loads.
+// them is read once per step and only displaces useful lines. The choice is made per
+// split (by its first key), so keep this a multiple of the split size. -1: never stream.
 #define PK_DECODE_NT_FROM 2048
 #endif
 
@@ -78,7 +79,9 @@ struct DecodeState {
 // lane's byte offset inside a token row. Keys past t_end re-read the step's last valid
 // row (same cache block, finite data) and consume() masks them to p = 0, so no load
 // needs a branch and all offsets past the wave-uniform base are the same per lane.
-template <int U, bool PAGED>
+// STREAM selects non-temporal loads; it is a template parameter (not a runtime branch)
+// so the pipelined loop stays straight-line and its wait counts stay exact.
+template <int U, bool PAGED, bool STREAM>
 __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_bytes, int b, int k0, int t,
                                             int t_end, uint4 (&kr)[U], uint4 (&vr)[U]) {
   const uint16_t* kp;
@@ -93,24 +96,34 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_byt
     kp = a.k + (int64_t)(k0 + t) * a.k_row_stride;
     vp = a.v + (int64_t)(k0 + t) * a.v_row_stride;
   }
+  // wave-uniform base + 32-bit per-lane offset: the scalar-base addressing form, no
+  // 64-bit vector address arithmetic (row strides are < 2^22 elements, checked on the host)
+  const char* kc = reinterpret_cast<const char*>(kp);
+  const char* vc = reinterpret_cast<const char*>(vp);
+  const uint32_t k_row_bytes = (uint32_t)a.k_row_stride * 2u;
+  const uint32_t v_row_bytes = (uint32_t)a.v_row_stride * 2u;
   const int last = t_end - 1 - t;
-  const bool stream = PK_DECODE_NT_FROM >= 0 && t >= PK_DECODE_NT_FROM;  // wave-uniform
-  if (stream) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      kr[u] = load16_stream(reinterpret_cast<const char*>(kp + (int64_t)min(u, last) * a.k_row_stride) + lane_bytes);
+  for (int u = 0; u < U; ++u) {
+    const char* row = kc + (__umul24((uint32_t)min(u, last), k_row_bytes) + lane_bytes);
+    kr[u] = STREAM ? load16_stream(row) : load16(row);
+  }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      vr[u] = load16_stream(reinterpret_cast<const char*>(vp + (int64_t)min(u, last) * a.v_row_stride) + lane_bytes);
-  } else {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      kr[u] = load16(reinterpret_cast<const char*>(kp + (int64_t)min(u, last) * a.k_row_stride) + lane_bytes);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      vr[u] = load16(reinterpret_cast<const char*>(vp + (int64_t)min(u, last) * a.v_row_stride) + lane_bytes);
+  for (int u = 0; u < U; ++u) {
+    const char* row = vc + (__umul24((uint32_t)min(u, last), v_row_bytes) + lane_bytes);
+    vr[u] = STREAM ? load16_stream(row) : load16(row);
   }
 }
+
+// Keys [t_begin, t_end) of one split through a two-stage software pipeline: the loads of
+// step n+1 are in flight while step n is consumed. The prefetch is unconditional (past
+// t_end it re-reads the current step, which hits in cache) so the code is straight-line
+// and the wait counts stay exact. The scheduling barriers keep each step's loads together
+// ahead of its math: otherwise the scheduler sinks every load next to its first use to
+// save registers, which serialises their latency.
+template <int G, int U, bool PAGED, bool STREAM>
+__device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
+                                             int k0, int t_begin, int t_end);
 
 // Fold keys [t, t + U) (already loaded) into the running softmax state.
 template <int G, int U>
@@ -178,6 +191,25 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
   }
 }
 
+template <int G, int U, bool PAGED, bool STREAM>
+__device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
+                                             int k0, int t_begin, int t_end) {
+  const float c2 = a.scale_log2;
+  uint4 kA[U], vA[U], kB[U], vB[U];
+  issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
+  for (int t = t_begin; t < t_end; t += 2 * U) {
+    const int t1 = t + U;
+    issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    consume<G, U>(st, c2, t, t_end, kA, vA);
+    if (t1 >= t_end) break;
+    const int t2 = t1 + U;
+    issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    consume<G, U>(st, c2, t1, t_end, kB, vB);
+  }
+}
+
 template <int G, int U, bool PAGED>
 __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
   static_assert(U % 2 == 0, "P.V pairs keys");
@@ -221,24 +253,11 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
     for (int e = 0; e < 8; ++e) st.acc[i][e] = 0.f;
   }
 
-  // Two-stage software pipeline: the loads of step n+1 are in flight while step n is
-  // consumed. The prefetch is unconditional (past t_end it re-reads the current step,
-  // which hits in cache) so the wait counts stay exact. The scheduling barriers keep
-  // each step's loads together ahead of its math: otherwise the scheduler sinks every
-  // load next to its first use to save registers, which serialises their latency.
-  uint4 kA[U], vA[U], kB[U], vB[U];
-  issue_loads<U, PAGED>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
-  for (int t = t_begin; t < t_end; t += 2 * U) {
-    const int t1 = t + U;
-    issue_loads<U, PAGED>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
-    __builtin_amdgcn_sched_barrier(0);
-    consume<G, U>(st, c2, t, t_end, kA, vA);
-    if (t1 >= t_end) break;
-    const int t2 = t1 + U;
-    issue_loads<U, PAGED>(a, lane_bytes, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
-    __builtin_amdgcn_sched_barrier(0);
-    consume<G, U>(st, c2, t1, t_end, kB, vB);
-  }
+  const bool stream = PK_DECODE_NT_FROM >= 0 && t_begin >= PK_DECODE_NT_FROM;  // per work-group
+  if (stream)
+    decode_range<G, U, PAGED, true>(st, a, lane_bytes, b, k0, t_begin, t_end);
+  else
+    decode_range<G, U, PAGED, false>(st, a, lane_bytes, b, k0, t_begin, t_end);
 
   if (!row_live) return;
 #pragma unroll
