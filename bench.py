@@ -40,8 +40,24 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed_launches(fn, reps: int, warmup: int = 3):
-    """Mean and median GPU time (ms) of fn() measured with events on the current stream."""
+_FLUSH = None
+
+
+def flush_caches():
+    """Read 512 MiB so no K/V line of the previous launch is still in L2 or the 256 MB
+    Infinity Cache (in a real step the 27 other layers' KV pass through in between). A
+    read leaves clean lines, so the timed kernel pays no write-back for the flush."""
+    import torch
+
+    global _FLUSH
+    if _FLUSH is None:
+        _FLUSH = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+    _FLUSH.sum()
+
+
+def timed_launches(fn, reps: int, warmup: int = 3, cold: bool = True):
+    """Mean and median GPU time (ms) of fn() measured with events on the current stream;
+    cold=True flushes the caches before every launch (outside the timed interval)."""
     import torch
 
     for _ in range(warmup):
@@ -49,6 +65,8 @@ def timed_launches(fn, reps: int, warmup: int = 3):
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     for a, b in evs:
+        if cold:
+            flush_caches()
         a.record()
         fn()
         b.record()
@@ -128,8 +146,9 @@ def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
     med = statistics.median(times)
     return {"value": round(kv_bytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"CPU oracle (torch fp32, store + paged decode) on the first {len(ids)} of 256 "
-                      f"sequences ({kv_bytes / 1e9:.3f} GB of KV), median of {reps} runs = {med:.3f} s"}
+            "sample": f"CPU oracle (torch fp32 on {torch.get_num_threads()} threads, store + paged decode) "
+                      f"on {len(ids)} of the 256 sequences ({kv_bytes / 1e9:.3f} GB of KV), "
+                      f"median of {reps} runs = {med:.3f} s"}
 
 
 def main() -> int:
@@ -139,7 +158,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configurations")
-    ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only run 5 cfg2 decode calls and 5 copies of 1 GiB (the counter calibration), "
+                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the paged-KV path is not sharded across GPUs "
@@ -155,6 +177,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     log("[bench] building cfg2 (256 seqs, Lk ~ U[1024, 8192]) on the GPU")
     w = make_workload("cfg2", dev)
+    if args.pmc_probe:
+        return pmc_probe(w)
     kv_bytes = w.decode_kv_bytes()
     store_bytes = w.store_bytes()
     ctx = w.ctx
@@ -192,10 +216,12 @@ def main() -> int:
     achieved = kv_bytes / (attn_mean * 1e-3) / 1e9
     log(f"[bench] step {ms_per_step:.3f} ms, decode call {attn_mean:.3f} ms -> {achieved:.1f} GB/s")
 
+    # HBM bytes per decode call on this workload, measured with rocprofv3 --pmc
+    # FETCH_SIZE / WRITE_SIZE (calibrated on a copy of known size); recorded in profiles/
     traffic = None
     tfile = ROOT / "profiles" / "traffic.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("paged_decode_cfg2_bytes_per_launch")
+        traffic = json.loads(tfile.read_text()).get("cfg2_decode_call_hbm_bytes")
 
     result = {
         "metric": METRIC,
@@ -220,7 +246,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged decode attention call (split-K decode + combine)",
+            "kernel": "pk_varlen_attention decode call = decode_split_kernel + decode_combine_kernel",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -245,6 +271,26 @@ def main() -> int:
     return 0
 
 
+def pmc_probe(w) -> int:
+    """5 decode calls of the cfg2 batch, then 5 device copies of exactly 1 GiB: the copy
+    gives the factor between what FETCH_SIZE / WRITE_SIZE report and the bytes moved."""
+    import torch
+
+    import pagedkv
+
+    out = torch.empty_like(w.q)
+    for _ in range(5):
+        pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k, 1,
+                                 w.max_seqlen_k, SCALE, True, w.block_tables, out=out)
+    src = torch.ones(1 << 29, dtype=torch.int16, device=w.q.device)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": "done", "kv_bytes": w.decode_kv_bytes(), "copy_bytes": 1 << 30}), flush=True)
+    return 0
+
+
 def extra_configs(dev, w2):
     """Per-kernel measurements of the other configurations (events, mean of 20 launches)."""
     import torch
@@ -255,6 +301,7 @@ def extra_configs(dev, w2):
     res = {}
     # cfg2 store of the 256 new tokens
     ms, _ = timed_launches(lambda: pagedkv.store_kvcache(w2.k, w2.v, w2.k_cache, w2.v_cache, w2.slot_mapping), 20)
+    res["cache_state"] = "cold: 512 MiB read before every timed launch"
     res["cfg2_store"] = {"ms": round(ms, 5), "GB/s": round(w2.store_bytes() / ms / 1e6, 1)}
 
     log("[bench] cfg1")

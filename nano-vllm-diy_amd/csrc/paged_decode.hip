@@ -282,16 +282,35 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   }
 }
 
-// Merge the per-split partials of one (sequence, head): thread d owns element d. A
-// separate launch (rather than a "last work-group merges" tail in the split kernel) because
-// the XCD L2 caches are not coherent with each other: a device-scope fence per
-// work-group would write back and invalidate a whole L2, while the kernel boundary makes
-// every partial visible for free.
-__global__ __launch_bounds__(kHeadDim) void decode_combine_kernel(const AttnArgs a) {
+// Merge the per-split partials of one (sequence, head). A separate launch (rather than a
+// "last work-group merges" tail in the split kernel) because the XCD L2 caches are not
+// coherent with each other: a device-scope fence per work-group would write back and
+// invalidate a whole L2, while the kernel boundary makes every partial visible for free.
+// The split maxima and weights are computed in parallel across splits (block reductions),
+// then thread d forms the weighted sum of element d with four independent accumulators.
+constexpr int kCombineThreads = kHeadDim;  // thread d owns output element d
+constexpr int kCombineMaxSplits = 256;     // splits per sequence the weight table holds
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  for (int m = kWave / 2; m >= 1; m >>= 1) {
+    const float o = xor_shfl(v, m);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  const int wave = threadIdx.x / kWave;
+  __syncthreads();  // red may still be read by a previous reduction
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
+  __syncthreads();
+  v = red[0];
+  for (int w = 1; w < kCombineThreads / kWave; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
+  return v;
+}
+
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const AttnArgs a) {
   constexpr int D = kHeadDim;
+  __shared__ float w_s[kCombineMaxSplits];
+  __shared__ float red[kCombineThreads / kWave];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int d = threadIdx.x;
   const int q0 = a.cu_q[b];
   if (a.cu_q[b + 1] - q0 != 1) return;
   const int Lk = min(a.cu_k[b + 1] - a.cu_k[b], a.max_seqlen_k);
@@ -299,17 +318,31 @@ __global__ __launch_bounds__(kHeadDim) void decode_combine_kernel(const AttnArgs
   const int nsplit = (Lk + a.split_tokens - 1) / a.split_tokens;
   if (nsplit <= 1) return;  // written directly by the split kernel
   const int H = a.num_heads;
-  const int64_t unit0 = (int64_t)b * a.max_splits * H + h;
+  const int64_t unit0 = (int64_t)b * a.max_splits * H + h;  // partial of split j: unit0 + j H
   float mx = -INFINITY;
-  for (int j = 0; j < nsplit; ++j) mx = fmaxf(mx, a.part_ml[(unit0 + (int64_t)j * H) * 2]);
-  float lsum = 0.f, o = 0.f;
-  for (int j = 0; j < nsplit; ++j) {
-    const int64_t unit = unit0 + (int64_t)j * H;
-    const float w = exp2_fast(a.part_ml[unit * 2] - mx);
-    lsum = fmaf(w, a.part_ml[unit * 2 + 1], lsum);
-    o = fmaf(w, a.part_o[unit * D + d], o);
+  for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) mx = fmaxf(mx, a.part_ml[(unit0 + (int64_t)j * H) * 2]);
+  mx = block_reduce(mx, true, red);
+  float lsum = 0.f;
+  for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)j * H) * 2);
+    const float w = exp2_fast(ml.x - mx);
+    w_s[j] = w;
+    lsum = fmaf(w, ml.y, lsum);
   }
-  a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(o / lsum);
+  lsum = block_reduce(lsum, false, red);  // its barriers also publish w_s
+  const int d = threadIdx.x;
+  const float* po = a.part_o + unit0 * D + d;
+  const int64_t stride = (int64_t)H * D;
+  float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+  int j = 0;
+  for (; j + 4 <= nsplit; j += 4) {
+    o0 = fmaf(w_s[j], po[(int64_t)j * stride], o0);
+    o1 = fmaf(w_s[j + 1], po[(int64_t)(j + 1) * stride], o1);
+    o2 = fmaf(w_s[j + 2], po[(int64_t)(j + 2) * stride], o2);
+    o3 = fmaf(w_s[j + 3], po[(int64_t)(j + 3) * stride], o3);
+  }
+  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], po[(int64_t)j * stride], o0);
+  a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(((o0 + o1) + (o2 + o3)) / lsum);
 }
 
 template <int G, int U>
@@ -330,10 +363,14 @@ hipError_t launch_decode_g(const AttnArgs& a, bool paged, hipStream_t stream) {
 }  // namespace
 
 int decode_split_tokens(int num_seqs, int max_seqlen_k) {
-  // One 256-key cache block per work-group when the batch yields enough work-groups
-  // to cover the 256 CUs several times; shorter splits for small batches.
+  // PK_DECODE_SPLIT_MAX keys per work-group when the batch yields enough work-groups to
+  // cover the 256 CUs several times, shorter splits for small batches; longer ones when
+  // the combine pass's weight table (kCombineMaxSplits per sequence) would overflow.
+  const auto splits = [&](int split) { return (int64_t)(max_seqlen_k + split - 1) / split; };
   int split = PK_DECODE_SPLIT_MAX;
-  while (split > 64 && (int64_t)num_seqs * ((max_seqlen_k + split - 1) / split) < 2048) split /= 2;
+  while (split > 64 && (int64_t)num_seqs * splits(split) < 2048 && splits(split / 2) <= kCombineMaxSplits)
+    split /= 2;
+  while (splits(split) > kCombineMaxSplits) split *= 2;
   return split;
 }
 
@@ -351,7 +388,7 @@ hipError_t launch_decode(const AttnArgs& a, int group, bool paged, int max_seqle
   if (err != hipSuccess) return err;
   if (a.max_splits > 1) {
     hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)a.num_heads, (unsigned)a.num_seqs),
-                       dim3(kHeadDim), 0, stream, a);
+                       dim3(kCombineThreads), 0, stream, a);
     err = hipGetLastError();
   }
   return err;

@@ -1,0 +1,156 @@
+"""CPU tests of the host side: the C-ABI library (loads, exports, argument checks that
+return before any GPU work), the seeded workloads and their slot / block-table layout."""
+import ctypes
+import math
+import pathlib
+import re
+
+import pytest
+import torch
+
+from pagedkv import _lib
+from pagedkv.workloads import BLOCK_SIZE, HKV, HEAD_DIM, HQ, WORKLOADS, make_workload, slots_for
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "pagedkv.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.lib()
+    names = header_functions()
+    assert names, "no declarations parsed from include/pagedkv.h"
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in pagedkv.h but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
+    assert lib.pk_abi_version() == _lib.ABI_VERSION
+
+
+def test_error_codes_match_header():
+    text = HEADER.read_text()
+    for name in ("PK_OK", "PK_ERR_INVALID_ARG", "PK_ERR_UNSUPPORTED", "PK_ERR_WORKSPACE", "PK_ERR_HIP"):
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
+        assert m and int(m.group(1)) == getattr(_lib, name)
+
+
+def _attn(lib, **kw):
+    args = dict(q=None, q_row_stride=HQ * HEAD_DIM, k=None, v=None, k_row_stride=HKV * HEAD_DIM,
+                v_row_stride=HKV * HEAD_DIM, k_block_stride=BLOCK_SIZE * HKV * HEAD_DIM,
+                v_block_stride=BLOCK_SIZE * HKV * HEAD_DIM, block_table=None, bt_stride=0,
+                block_size=BLOCK_SIZE, cu_q=None, cu_k=None, num_seqs=1, max_q=1, max_k=1,
+                num_heads=HQ, num_kv_heads=HKV, head_dim=HEAD_DIM, scale=0.088, causal=1,
+                out=None, out_row_stride=HQ * HEAD_DIM, ws=None, ws_bytes=0, stream=None)
+    args.update(kw)
+    return lib.pk_varlen_attention(*args.values())
+
+
+def test_attention_argument_checks_fail_before_launch():
+    lib = _lib.lib()
+    assert _attn(lib, head_dim=64) == _lib.PK_ERR_UNSUPPORTED
+    assert b"head_dim" in lib.pk_last_error()
+    assert _attn(lib, num_heads=12, num_kv_heads=8) == _lib.PK_ERR_INVALID_ARG
+    assert _attn(lib, num_heads=24, num_kv_heads=8) == _lib.PK_ERR_UNSUPPORTED  # group 3
+    assert _attn(lib, num_seqs=-1) == _lib.PK_ERR_INVALID_ARG
+    assert _attn(lib, num_seqs=70000) == _lib.PK_ERR_INVALID_ARG
+    assert _attn(lib) == _lib.PK_ERR_INVALID_ARG  # null pointers
+    assert b"null" in lib.pk_last_error()
+    # nothing to do: success without touching any pointer
+    assert _attn(lib, num_seqs=0) == _lib.PK_OK
+    assert _attn(lib, max_q=0) == _lib.PK_OK
+
+
+def test_store_argument_checks_fail_before_launch():
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x10000)
+    assert lib.pk_store_kvcache(fake, 1024, fake, 1024, fake, fake, fake, 4, 1020, 0, None) == _lib.PK_ERR_INVALID_ARG
+    assert lib.pk_store_kvcache(fake, 1000, fake, 1024, fake, fake, fake, 4, 1024, 0, None) == _lib.PK_ERR_INVALID_ARG
+    odd = ctypes.c_void_p(0x10008)
+    assert lib.pk_store_kvcache(odd, 1024, fake, 1024, fake, fake, fake, 4, 1024, 0, None) == _lib.PK_ERR_INVALID_ARG
+    assert b"aligned" in lib.pk_last_error()
+    assert lib.pk_store_kvcache(None, 1024, None, 1024, None, None, None, 0, 1024, 0, None) == _lib.PK_OK
+
+
+def test_workspace_size_formula():
+    lib = _lib.lib()
+    # one split per sequence needs no workspace
+    assert lib.pk_varlen_attention_workspace_bytes(8, HQ, HEAD_DIM, 1, 64) == 0
+    ws = lib.pk_varlen_attention_workspace_bytes(256, HQ, HEAD_DIM, 1, 8192)
+    split = 512
+    units = 256 * (8192 // split) * HQ
+    want = math.ceil(units * HEAD_DIM * 4 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
+    assert ws == want
+
+
+def test_workloads_are_deterministic_and_well_formed():
+    for name in WORKLOADS:
+        a = make_workload(name, "cpu", num_seqs=4)
+        b = make_workload(name, "cpu", num_seqs=4)
+        assert torch.equal(a.block_tables, b.block_tables)
+        assert torch.equal(a.slot_mapping, b.slot_mapping)
+        assert torch.equal(a.q.view(torch.int16), b.q.view(torch.int16))
+        assert a.cu_seqlens_q.dtype == torch.int32 and a.block_tables.dtype == torch.int32
+        assert int(a.cu_seqlens_q[-1]) == a.q.shape[0] == a.k.shape[0] == a.slot_mapping.numel()
+        # v is a strided view into the fused qkv row, as at the Qwen3 call site
+        assert a.v.stride(0) == (HQ + 2 * HKV) * HEAD_DIM and a.v.stride(1) == HEAD_DIM
+        assert a.k.is_contiguous() and a.q.is_contiguous()
+
+
+@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4"])
+def test_block_tables_and_slots(name):
+    w = make_workload(name, "cpu", num_seqs=6)
+    bt = w.block_tables.tolist()
+    used = []
+    for b, (lq, lk) in enumerate(zip(w.q_lens, w.k_lens)):
+        nb = math.ceil(lk / BLOCK_SIZE)
+        assert all(x >= 0 for x in bt[b][:nb]) and all(x == -1 for x in bt[b][nb:])
+        used.append(bt[b][:nb])
+    # slots of each sequence's new tokens follow the block-table walk (model_runner.py:200-210)
+    slots = w.slot_mapping.tolist()
+    pos = 0
+    for b, (lq, lk) in enumerate(zip(w.q_lens, w.k_lens)):
+        assert slots[pos:pos + lq] == slots_for(bt[b], lk - lq, lk)
+        pos += lq
+    flat = [x for t in used for x in t]
+    if name == "cfg4":
+        shared = w.meta["shared_blocks"]
+        assert all(t[:len(shared)] == shared for t in used)
+        private = [x for t in used for x in t[len(shared):]]
+        assert len(set(private)) == len(private) and not set(private) & set(shared)
+    else:
+        assert len(set(flat)) == len(flat), "private blocks are never shared"
+    assert len(set(slots)) == len(slots), "no two new tokens share a slot"
+
+
+def test_slots_for_closed_form():
+    bt = [7, 3, 9]
+    assert slots_for(bt, 0, 3) == [7 * 256, 7 * 256 + 1, 7 * 256 + 2]
+    assert slots_for(bt, 255, 258) == [7 * 256 + 255, 3 * 256, 3 * 256 + 1]
+    assert slots_for(bt, 700, 701) == [9 * 256 + 188]
+
+
+def test_algorithmic_work_formulas():
+    w = make_workload("cfg3", "cpu", num_seqs=4)
+    row = HKV * HEAD_DIM * 2
+    assert w.decode_kv_bytes() == sum(lk * 2 * row for lq, lk in zip(w.q_lens, w.k_lens) if lq == 1)
+    fl = 0
+    for lq, lk in zip(w.q_lens, w.k_lens):
+        if lq > 1:
+            p = lk - lq
+            # causal: row i sees p + i + 1 keys; QK and PV are 2 flops per MAC each
+            fl += sum(2 * 2 * HQ * HEAD_DIM * (p + i + 1) for i in range(lq))
+    assert w.prefill_flops() == fl
+    n = w.slot_mapping.numel()
+    assert w.store_bytes() == 4 * n * row + 4 * n
+
+
+def test_attention_module_mirrors_reference_constructor():
+    import pagedkv
+
+    layer = pagedkv.Attention(128, 16, 8, 128 ** -0.5)
+    assert (layer.head_dim, layer.num_heads, layer.num_kv_heads) == (128, 16, 8)
+    assert layer.k_cache.numel() == 0 and layer.v_cache.numel() == 0
+    ctx = pagedkv.Context()
+    assert ctx.block_tables is None and ctx.max_seqlen_q == 0

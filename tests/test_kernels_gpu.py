@@ -341,3 +341,29 @@ def test_workspace_reuse_across_batch_shapes(gpu):
             got = run(w)
             torch.cuda.synchronize()
             assert bits_equal(got, want), f"{w.name} rep {rep}"
+
+
+def test_long_context_small_batch(gpu):
+    """40k-key sequences: decode splits grow to fit the combine table, and the prefill
+    kernel reads block ids past the 64 it keeps in a register."""
+    g = torch.Generator(device=gpu).manual_seed(21)
+    seqs = [(1, 40000), (70, 33000), (1, 300)]
+    nb_per = [math.ceil(lk / BLOCK_SIZE) for _, lk in seqs]
+    nb = sum(nb_per)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(4)).tolist()
+    bt = torch.full((len(seqs), max(nb_per)), -1, dtype=torch.int32)
+    pos = 0
+    for i, c in enumerate(nb_per):
+        bt[i, :c] = torch.tensor(perm[pos:pos + c])
+        pos += c
+    nq = sum(s[0] for s in seqs)
+    q = torch.randn(nq, 16, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    kc = torch.randn(nb, BLOCK_SIZE, 8, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    vc = torch.randn(nb, BLOCK_SIZE, 8, 128, generator=g, device=gpu, dtype=torch.bfloat16)
+    cu_q = torch.tensor([0] + np.cumsum([s[0] for s in seqs]).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + np.cumsum([s[1] for s in seqs]).tolist(), dtype=torch.int32)
+    out = pagedkv.varlen_attention(q, kc, vc, cu_q.to(gpu), cu_k.to(gpu), 70, 40000, None, True,
+                                   bt.to(gpu))
+    want = oracle.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q, cu_k, None, True, bt)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, want, "long context")
