@@ -217,9 +217,14 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
   // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
-  const int g_first = (blockIdx.z * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
-  const int b = blockIdx.y;
-  const int split = blockIdx.x;
+  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
+  // Work-groups are dispatched round-robin over the 8 XCDs in linear id order. Split-major
+  // order with the sequence rotated by the split index sends consecutive splits of one
+  // sequence to consecutive XCDs, so every XCD gets about 1/8 of each sequence whatever the
+  // lengths (a (split, sequence) grid with 16 splits would give XCD k splits k and k+8 of
+  // every sequence: split 0 always exists, split 15 only for the longest contexts).
+  const int split = blockIdx.x / a.num_seqs;
+  const int b = (blockIdx.x - split * a.num_seqs + split) % a.num_seqs;
   const int q0 = a.cu_q[b];
   if (a.cu_q[b + 1] - q0 != 1) return;  // rows with Lq != 1 belong to the prefill kernel
   const int k0 = a.cu_k[b];
@@ -351,7 +356,7 @@ hipError_t launch_decode_g(const AttnArgs& a, bool paged, hipStream_t stream) {
   int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
   while (quads % waves != 0) --waves;            // no idle wavefront in any work-group
   const int zgroups = quads / waves;
-  const dim3 grid((unsigned)a.max_splits, (unsigned)a.num_seqs, (unsigned)zgroups);
+  const dim3 grid((unsigned)(a.max_splits * a.num_seqs), (unsigned)zgroups);
   const dim3 block((unsigned)(waves * kWave));
   if (paged)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true>), grid, block, 0, stream, a);
