@@ -291,6 +291,37 @@ def pmc_probe(w) -> int:
     return 0
 
 
+def producer_call(dev, n: int, seed: int = 6):
+    """Fused q/k norm + RoPE + K/V store for n tokens of the Qwen3-0.6B attention geometry.
+
+    Algorithmic bytes per token: the fused qkv row (Hq + 2 Hkv) D 2 B read, q (Hq D 2 B)
+    and the K and V cache rows (2 Hkv D 2 B) written, the position (8 B), the slot (4 B)
+    and the token's fp32 cos/sin row (D 4 B) read.
+    """
+    import torch
+
+    import pagedkv
+    from pagedkv.workloads import BLOCK_SIZE, HEAD_DIM, HKV, HQ
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    qkv = torch.randn(n, (HQ + 2 * HKV) * HEAD_DIM, generator=g, device=dev).to(torch.bfloat16)
+    cs = pagedkv.rope_cos_sin(40960, HEAD_DIM, 1000000.0, dev)
+    pos = torch.randint(0, 40960, (n,), generator=g, device=dev)
+    nb = (n + BLOCK_SIZE - 1) // BLOCK_SIZE * 2
+    kc = torch.empty(nb, BLOCK_SIZE, HKV, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    slots = torch.randperm(nb * BLOCK_SIZE, generator=g, device=dev)[:n].to(torch.int32)
+    qw = torch.ones(HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    kw = torch.ones(HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    q_out = torch.empty(n, HQ, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    per_token = (HQ + 2 * HKV) * HEAD_DIM * 2 + HQ * HEAD_DIM * 2 + 2 * HKV * HEAD_DIM * 2 + 8 + 4 + HEAD_DIM * 4
+
+    def fn():
+        pagedkv.qk_norm_rope_store(qkv, pos, cs, HQ, HKV, HEAD_DIM, qw, kw, 1e-6, kc, vc, slots,
+                                   q_out=q_out)
+    return fn, n * per_token
+
+
 def extra_configs(dev, w2):
     """Per-kernel measurements of the other configurations (events, mean of 20 launches)."""
     import torch
@@ -324,6 +355,13 @@ def extra_configs(dev, w2):
     ms_d, _ = timed_launches(attention_call(w3, sub_batch(w3, lambda i: w3.q_lens[i] == 1)), 20)
     kvb = w3.decode_kv_bytes()
     res["cfg3_decode"] = {"ms": round(ms_d, 5), "GB/s": round(kvb / ms_d / 1e6, 1), "seqs": n_dec}
+
+    log("[bench] producer")
+    for n in (256, 16384):
+        fn, nbytes = producer_call(dev, n)
+        ms, _ = timed_launches(fn, 20)
+        res[f"producer_{n}"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+                                "bytes": nbytes}
 
     log("[bench] cfg4")
     w4 = make_workload("cfg4", dev)

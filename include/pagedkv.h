@@ -155,6 +155,40 @@ int pk_gather_kv(const void* cache, int64_t block_stride, int32_t block_size,
                  const int32_t* cu_seqlens_k, int32_t num_seqs, int32_t max_seqlen_k,
                  int32_t row_elems, void* dst, pk_stream_t stream);
 
+/*
+ * pk_qk_norm_rope_store -- the producer of the attention inputs, fused: replaces
+ * q_norm / k_norm (RMSNorm over head_dim, src/layers/layernorm.py:11-16),
+ * rotary_emb (rotate-half RoPE, src/layers/pos_embedding.py:30-48) and the
+ * store_kvcache call (src/layers/attention.py:87-88) as run by
+ * Qwen3Attention.forward (src/models/qwen3.py:80-89).
+ *
+ *   qkv  (num_tokens, (num_heads + 2 num_kv_heads) * head_dim) bf16, the fused
+ *        projection output [q heads | k heads | v heads], row stride
+ *        qkv_row_stride.
+ *   positions (num_tokens,) int64; cos_sin (max_position, head_dim) fp32, row p =
+ *        [cos(p f_0..f_63) | sin(p f_0..f_63)] (pos_embedding.py:6-18). Positions
+ *        outside [0, max_position) are clamped (the reference would index out of
+ *        range).
+ *   q_norm_weight, k_norm_weight (head_dim,) bf16, or NULL to skip the norm (the
+ *        qkv_bias variant, qwen3.py:85).
+ * For every token i and head h:
+ *   x  = bf16(w * (x * rsqrt(mean(x^2) + eps)))          (fp32 inside)
+ *   q_out[i, h]  = bf16(rope(x, positions[i]))            (fp32 inside)
+ * and the same for k heads, written to k_out (if non-NULL, for attention over
+ * fresh keys) and, when the caches are non-NULL and slot_mapping[i] != -1, to
+ * k_cache[slot]; the raw v row goes to v_cache[slot]. num_slots > 0 drops slots
+ * outside [0, num_slots) (no reference counterpart, as in pk_store_kvcache).
+ * Built for head_dim 128; all tensors 16-byte aligned, strides multiples of 8.
+ */
+int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride,
+                          const int64_t* positions, const float* cos_sin, int64_t max_position,
+                          const void* q_norm_weight, const void* k_norm_weight, float eps,
+                          int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_dim, void* q_out, int64_t q_out_row_stride,
+                          void* k_out, int64_t k_out_row_stride,
+                          void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                          int64_t num_slots, pk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

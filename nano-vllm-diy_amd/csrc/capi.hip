@@ -65,7 +65,7 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
 
 extern "C" {
 
-int pk_abi_version(void) { return 1; }
+int pk_abi_version(void) { return 2; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -219,6 +219,52 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
   if (max_seqlen_q > 1)
     rc = hip_status(pk::launch_prefill(a, group, paged, causal != 0, max_seqlen_q, s), "prefill launch");
   return rc;
+}
+
+int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,
+                          const float* cos_sin, int64_t max_position, const void* q_norm_weight,
+                          const void* k_norm_weight, float eps, int32_t num_tokens,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, void* q_out,
+                          int64_t q_out_row_stride, void* k_out, int64_t k_out_row_stride,
+                          void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                          int64_t num_slots, pk_stream_t stream) {
+  g_last_error.clear();
+  if (head_dim != pk::kHeadDim)
+    return fail(PK_ERR_UNSUPPORTED, "qk_norm_rope_store: head_dim=%d not built (only %d)", head_dim, pk::kHeadDim);
+  if (num_tokens < 0) return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: num_tokens=%d < 0", num_tokens);
+  if (num_heads <= 0 || num_kv_heads <= 0)
+    return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: num_heads=%d, num_kv_heads=%d must be positive",
+                num_heads, num_kv_heads);
+  if (num_tokens == 0) return PK_OK;
+  if (!qkv || !positions || !cos_sin || !q_out)
+    return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: null qkv / positions / cos_sin / q_out");
+  if ((k_cache == nullptr) != (v_cache == nullptr))
+    return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: pass both caches or neither");
+  if (k_cache && !slot_mapping) return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: null slot_mapping");
+  if (max_position <= 0) return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: max_position must be positive");
+  if (!(eps >= 0.f)) return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: eps must be >= 0");
+  if (num_slots < 0) return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: num_slots < 0");
+  const int64_t row = (int64_t)(num_heads + 2 * num_kv_heads) * head_dim;
+  if (qkv_row_stride < row || qkv_row_stride % 8 != 0)
+    return fail(PK_ERR_INVALID_ARG, "qkv_row_stride=%lld must be >= %lld and a multiple of 8",
+                (long long)qkv_row_stride, (long long)row);
+  if (q_out_row_stride < (int64_t)num_heads * head_dim || q_out_row_stride % 8 != 0)
+    return fail(PK_ERR_INVALID_ARG, "q_out_row_stride=%lld must be >= %d and a multiple of 8",
+                (long long)q_out_row_stride, num_heads * head_dim);
+  if (k_out && (k_out_row_stride < (int64_t)num_kv_heads * head_dim || k_out_row_stride % 8 != 0))
+    return fail(PK_ERR_INVALID_ARG, "k_out_row_stride=%lld must be >= %d and a multiple of 8",
+                (long long)k_out_row_stride, num_kv_heads * head_dim);
+  if (!aligned16(qkv) || !aligned16(q_out) || (k_out && !aligned16(k_out)) ||
+      (k_cache && (!aligned16(k_cache) || !aligned16(v_cache))) || !aligned16(cos_sin) ||
+      (q_norm_weight && !aligned16(q_norm_weight)) || (k_norm_weight && !aligned16(k_norm_weight)))
+    return fail(PK_ERR_INVALID_ARG, "qk_norm_rope_store: tensors must be 16-byte aligned");
+  return hip_status(pk::launch_qk_norm_rope_store(qkv, qkv_row_stride, positions, cos_sin, max_position,
+                                                  q_norm_weight, k_norm_weight, eps, num_tokens,
+                                                  num_heads, num_kv_heads, q_out, q_out_row_stride,
+                                                  k_out, k_out_row_stride, k_cache, v_cache,
+                                                  slot_mapping, num_slots,
+                                                  reinterpret_cast<hipStream_t>(stream)),
+                    "qk_norm_rope_store launch");
 }
 
 }  // extern "C"

@@ -99,4 +99,14 @@ hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal,
                           int max_seqlen_q, hipStream_t stream);
 // Split size (keys per work-group) the decode kernel uses for these launch bounds.
 int decode_split_tokens(int num_seqs, int max_seqlen_k);
+// Per-head RMSNorm + RoPE of q and k from the fused qkv row, K/V rows into their slots.
+hipError_t launch_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride,
+                                     const int64_t* positions, const float* cos_sin,
+                                     int64_t max_position, const void* q_norm_weight,
+                                     const void* k_norm_weight, float eps, int32_t num_tokens,
+                                     int32_t num_heads, int32_t num_kv_heads, void* q_out,
+                                     int64_t q_out_row_stride, void* k_out,
+                                     int64_t k_out_row_stride, void* k_cache, void* v_cache,
+                                     const int32_t* slot_mapping, int64_t num_slots,
+                                     hipStream_t stream);
 }  // namespace pk

@@ -4,11 +4,14 @@ Public surface (mirrors the reference's src/layers/attention.py and
 src/utils/context.py):
     Attention, store_kvcache, Context,
     varlen_attention (flash_attn_varlen_func semantics), gather_kv,
-    workspace_bytes, reserve_workspace.
+    workspace_bytes, reserve_workspace,
+    qk_norm_rope_store + rope_cos_sin (the fused q/k norm, RoPE and cache store of
+    src/models/qwen3.py:80-89).
 """
 from .attention import Attention, store_kvcache  # noqa: F401
 from .context import Context  # noqa: F401
-from .ops import gather_kv, reserve_workspace, varlen_attention, workspace_bytes  # noqa: F401
+from .ops import (gather_kv, qk_norm_rope_store, reserve_workspace, rope_cos_sin,  # noqa: F401
+                  varlen_attention, workspace_bytes)
 
 __all__ = ["Attention", "store_kvcache", "Context", "varlen_attention", "gather_kv",
-           "workspace_bytes", "reserve_workspace"]
+           "workspace_bytes", "reserve_workspace", "qk_norm_rope_store", "rope_cos_sin"]

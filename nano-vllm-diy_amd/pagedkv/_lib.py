@@ -45,9 +45,17 @@ SIGNATURES = {
     "pk_gather_kv": (ctypes.c_int, [
         _c_void_p, _i64, _i32, _c_void_p, _i32, _c_void_p, _i32, _i32, _i32, _c_void_p,
         _c_void_p]),
+    "pk_qk_norm_rope_store": (ctypes.c_int, [
+        _c_void_p, _i64,                    # qkv, qkv_row_stride
+        _c_void_p, _c_void_p, _i64,         # positions, cos_sin, max_position
+        _c_void_p, _c_void_p, ctypes.c_float,  # q/k norm weights, eps
+        _i32, _i32, _i32, _i32,             # num_tokens, num_heads, num_kv_heads, head_dim
+        _c_void_p, _i64, _c_void_p, _i64,   # q_out, its row stride, k_out, its row stride
+        _c_void_p, _c_void_p, _c_void_p,    # k_cache, v_cache, slot_mapping
+        _i64, _c_void_p]),                  # num_slots, stream
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

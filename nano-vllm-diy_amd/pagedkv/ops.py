@@ -202,3 +202,86 @@ def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_k: torc
         block_table.stride(0), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_k), row,
         dst.data_ptr(), _stream(cache)), "pk_gather_kv")
     return dst
+
+
+def rope_cos_sin(max_position: int, head_dim: int, base: float = 1000000.0,
+                 device: torch.device | str = "cuda") -> torch.Tensor:
+    """The (max_position, head_dim) fp32 RoPE table [cos | sin] of position x frequency.
+
+    Built the way build_rope_cos_sin does it (src/layers/pos_embedding.py:6-18), as data
+    for qk_norm_rope_store; the reference's (P, 1, D) view is accepted there as well.
+    """
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
+    pos = torch.arange(max_position, dtype=torch.float, device=device)
+    freqs = torch.outer(pos, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).contiguous()
+
+
+def qk_norm_rope_store(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: torch.Tensor,
+                       num_heads: int, num_kv_heads: int, head_dim: int = 128,
+                       q_norm_weight: torch.Tensor | None = None,
+                       k_norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                       k_cache: torch.Tensor | None = None, v_cache: torch.Tensor | None = None,
+                       slot_mapping: torch.Tensor | None = None, return_k: bool = False,
+                       check_slots: bool = False, q_out: torch.Tensor | None = None,
+                       k_out: torch.Tensor | None = None):
+    """Fused q/k RMSNorm + RoPE + K/V cache store from the fused qkv projection output.
+
+    Replaces, in one kernel, the sequence of Qwen3Attention.forward
+    (src/models/qwen3.py:80-89): split of qkv, q_norm / k_norm (layernorm.py:11-16),
+    rotary_emb (pos_embedding.py:30-48) and the store inside Attention.forward
+    (attention.py:87-88). qkv (N, (Hq + 2 Hkv) D) bf16; positions (N,) int64;
+    cos_sin from rope_cos_sin. With caches given, K (normed, rotated) and raw V rows go
+    to slot_mapping's slots (-1 skips). Returns (q (N, Hq, D), k (N, Hkv, D) or None);
+    k is produced when return_k (attention over fresh keys needs it).
+    """
+    if qkv.dim() != 2 or qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be (N, (Hq + 2 Hkv) * D) bf16 with contiguous rows")
+    n = qkv.shape[0]
+    dev = qkv.device
+    if qkv.shape[1] != (num_heads + 2 * num_kv_heads) * head_dim:
+        raise ValueError(f"qkv width {qkv.shape[1]} != (Hq + 2 Hkv) * D")
+    if positions.dtype != torch.int64 or positions.device != dev or positions.numel() != n or \
+            not positions.is_contiguous():
+        raise ValueError("positions must be a contiguous (N,) int64 tensor on the qkv device")
+    if cos_sin.dim() == 3:
+        cos_sin = cos_sin.squeeze(1)
+    if cos_sin.dtype != torch.float32 or cos_sin.shape[-1] != head_dim or \
+            not cos_sin.is_contiguous() or cos_sin.device != dev:
+        raise ValueError("cos_sin must be a contiguous (P, D) float32 table on the qkv device")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w is not None and (w.dtype != torch.bfloat16 or w.numel() != head_dim or
+                              not w.is_contiguous() or w.device != dev):
+            raise ValueError(f"{name} must be a contiguous ({head_dim},) bf16 tensor on the qkv device")
+    if (k_cache is None) != (v_cache is None):
+        raise ValueError("pass both caches or neither")
+    row = num_kv_heads * head_dim
+    num_slots = 0
+    if k_cache is not None:
+        if slot_mapping is None:
+            raise ValueError("slot_mapping is required with caches")
+        _req_i32("slot_mapping", slot_mapping, dev)
+        assert slot_mapping.numel() == n and slot_mapping.is_contiguous()
+        for c in (k_cache, v_cache):
+            if c.dtype != torch.bfloat16 or c.device != dev or c.stride(-1) != 1 or \
+                    c.stride(-2) != head_dim or c.stride(1) != row or c.shape[-2] != num_kv_heads:
+                raise ValueError("caches must be (NB, BS, Hkv, D) bf16 with contiguous token rows")
+        if check_slots:
+            num_slots = k_cache.numel() // row
+    if q_out is None:
+        q_out = torch.empty(n, num_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    elif q_out.shape != (n, num_heads, head_dim) or q_out.stride(1) != head_dim or q_out.stride(2) != 1:
+        raise ValueError("q_out must be (N, Hq, D) with contiguous heads")
+    if return_k and k_out is None:
+        k_out = torch.empty(n, num_kv_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    if k_out is not None and (k_out.shape != (n, num_kv_heads, head_dim) or
+                              k_out.stride(1) != head_dim or k_out.stride(2) != 1):
+        raise ValueError("k_out must be (N, Hkv, D) with contiguous heads")
+    ptr = lambda t: t.data_ptr() if t is not None else 0  # noqa: E731
+    check(lib().pk_qk_norm_rope_store(
+        qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
+        ptr(q_norm_weight), ptr(k_norm_weight), float(eps), n, num_heads, num_kv_heads, head_dim,
+        q_out.data_ptr(), q_out.stride(0), ptr(k_out), k_out.stride(0) if k_out is not None else 0,
+        ptr(k_cache), ptr(v_cache), ptr(slot_mapping), num_slots, _stream(qkv)),
+        "pk_qk_norm_rope_store")
+    return q_out, k_out

@@ -154,3 +154,30 @@ def test_attention_module_mirrors_reference_constructor():
     assert layer.k_cache.numel() == 0 and layer.v_cache.numel() == 0
     ctx = pagedkv.Context()
     assert ctx.block_tables is None and ctx.max_seqlen_q == 0
+
+
+def _prod(lib, **kw):
+    fake = ctypes.c_void_p(0x10000)
+    args = dict(qkv=fake, qkv_row_stride=32 * HEAD_DIM, positions=fake, cos_sin=fake, max_position=4096,
+                qw=None, kw=None, eps=1e-6, n=4, hq=HQ, hkv=HKV, head_dim=HEAD_DIM, q_out=fake,
+                q_out_row_stride=HQ * HEAD_DIM, k_out=None, k_out_row_stride=0, k_cache=None,
+                v_cache=None, slots=None, num_slots=0, stream=None)
+    args.update(kw)
+    return lib.pk_qk_norm_rope_store(*args.values())
+
+
+def test_producer_argument_checks_fail_before_launch():
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x10000)
+    assert _prod(lib, head_dim=64) == _lib.PK_ERR_UNSUPPORTED
+    assert _prod(lib, n=-1) == _lib.PK_ERR_INVALID_ARG
+    assert _prod(lib, n=0) == _lib.PK_OK
+    assert _prod(lib, qkv=None) == _lib.PK_ERR_INVALID_ARG
+    assert _prod(lib, k_cache=fake) == _lib.PK_ERR_INVALID_ARG          # one cache only
+    assert b"both caches" in lib.pk_last_error()
+    assert _prod(lib, k_cache=fake, v_cache=fake) == _lib.PK_ERR_INVALID_ARG  # no slot_mapping
+    assert _prod(lib, qkv_row_stride=31 * HEAD_DIM) == _lib.PK_ERR_INVALID_ARG
+    assert _prod(lib, qkv=ctypes.c_void_p(0x10008)) == _lib.PK_ERR_INVALID_ARG
+    assert b"aligned" in lib.pk_last_error()
+    assert _prod(lib, max_position=0) == _lib.PK_ERR_INVALID_ARG
+    assert _prod(lib, eps=-1.0) == _lib.PK_ERR_INVALID_ARG
