@@ -189,6 +189,42 @@ int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride,
                           void* k_cache, void* v_cache, const int32_t* slot_mapping,
                           int64_t num_slots, pk_stream_t stream);
 
+/*
+ * Kernels of the serving loop around the attention path (used by the end-to-end engine).
+ *
+ * pk_add_rmsnorm -- RMSNorm.forward (src/layers/layernorm.py:30-39): with residual == NULL,
+ *   out = bf16(w * (x * rsqrt(mean(x^2) + eps))) (normal_forward, :11-16); otherwise
+ *   s = x + residual in fp32, out = bf16(w * (s * rsqrt(mean(s^2) + eps))) and
+ *   residual_out = bf16(s) (residual_forward, :18-28). bf16 rows of `hidden` <= 4096
+ *   elements (multiple of 8); out / residual_out may alias x / residual.
+ */
+int pk_add_rmsnorm(const void* x, int64_t x_row_stride, const void* residual,
+                   int64_t residual_row_stride, const void* weight, float eps, int32_t rows,
+                   int32_t hidden, void* out, int64_t out_row_stride, void* residual_out,
+                   int64_t residual_out_row_stride, pk_stream_t stream);
+
+/*
+ * pk_silu_and_mul -- SiluAndMul.forward (src/layers/activation.py:6-10):
+ *   out[r, c] = bf16(silu(x[r, c]) * x[r, inter + c]), computed in fp32 (the compiled
+ *   reference fuses both and rounds once). inter a multiple of 8.
+ */
+int pk_silu_and_mul(const void* x, int64_t x_row_stride, int32_t rows, int32_t inter, void* out,
+                    int64_t out_row_stride, pk_stream_t stream);
+
+/*
+ * pk_lm_head_greedy -- ParallelLMHead.forward (src/layers/llm_head.py:60-64) followed by a
+ * greedy choice (the reference samples, sampler.py:14-16; the serving benchmark runs greedy):
+ *   row m = hidden_states[cu_seqlens_q[m+1] - 1] when cu_seqlens_q != NULL (prefill: the
+ *   last token of each sequence, llm_head.py:61-63), else hidden_states[m];
+ *   token_ids[m] = argmax_v bf16(row . weight[v]) with the lowest v among equal maxima
+ *   (argmax over the reference's bf16 logits). The logits are never written.
+ *   keys: scratch of `rows` 64-bit words (no initial contents needed). hidden a multiple
+ *   of 128; weight (vocab, hidden) bf16 rows.
+ */
+int pk_lm_head_greedy(const void* hidden_states, int64_t row_stride, const int32_t* cu_seqlens_q,
+                      const void* weight, int64_t weight_row_stride, int32_t rows, int32_t vocab,
+                      int32_t hidden, uint64_t* keys, int32_t* token_ids, pk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,7 +65,7 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
 
 extern "C" {
 
-int pk_abi_version(void) { return 2; }
+int pk_abi_version(void) { return 3; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -265,6 +265,67 @@ int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_t
                                                   slot_mapping, num_slots,
                                                   reinterpret_cast<hipStream_t>(stream)),
                     "qk_norm_rope_store launch");
+}
+
+int pk_add_rmsnorm(const void* x, int64_t x_row_stride, const void* residual,
+                   int64_t residual_row_stride, const void* weight, float eps, int32_t rows,
+                   int32_t hidden, void* out, int64_t out_row_stride, void* residual_out,
+                   int64_t residual_out_row_stride, pk_stream_t stream) {
+  g_last_error.clear();
+  if (rows < 0) return fail(PK_ERR_INVALID_ARG, "add_rmsnorm: rows=%d < 0", rows);
+  if (rows == 0) return PK_OK;
+  if (hidden <= 0 || hidden % 8 != 0 || hidden > 4096)
+    return fail(PK_ERR_UNSUPPORTED, "add_rmsnorm: hidden=%d must be a multiple of 8 and <= 4096", hidden);
+  if (!x || !weight || !out || (residual && !residual_out))
+    return fail(PK_ERR_INVALID_ARG, "add_rmsnorm: null x / weight / out, or residual without residual_out");
+  if (x_row_stride < hidden || out_row_stride < hidden || x_row_stride % 8 || out_row_stride % 8 ||
+      (residual && (residual_row_stride < hidden || residual_row_stride % 8 ||
+                    residual_out_row_stride < hidden || residual_out_row_stride % 8)))
+    return fail(PK_ERR_INVALID_ARG, "add_rmsnorm: row strides must be >= hidden and multiples of 8");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) ||
+      (residual && (!aligned16(residual) || !aligned16(residual_out))))
+    return fail(PK_ERR_INVALID_ARG, "add_rmsnorm: tensors must be 16-byte aligned");
+  return hip_status(pk::launch_add_rmsnorm(x, x_row_stride, residual, residual_row_stride, weight, eps,
+                                           rows, hidden, out, out_row_stride, residual_out,
+                                           residual_out_row_stride, reinterpret_cast<hipStream_t>(stream)),
+                    "add_rmsnorm launch");
+}
+
+int pk_silu_and_mul(const void* x, int64_t x_row_stride, int32_t rows, int32_t inter, void* out,
+                    int64_t out_row_stride, pk_stream_t stream) {
+  g_last_error.clear();
+  if (rows < 0) return fail(PK_ERR_INVALID_ARG, "silu_and_mul: rows=%d < 0", rows);
+  if (rows == 0) return PK_OK;
+  if (inter <= 0 || inter % 8 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "silu_and_mul: width %d must be a positive multiple of 8", inter);
+  if (!x || !out) return fail(PK_ERR_INVALID_ARG, "silu_and_mul: null pointer argument");
+  if (x_row_stride < 2 * (int64_t)inter || x_row_stride % 8 || out_row_stride < inter || out_row_stride % 8)
+    return fail(PK_ERR_INVALID_ARG, "silu_and_mul: bad row strides");
+  if (!aligned16(x) || !aligned16(out)) return fail(PK_ERR_INVALID_ARG, "silu_and_mul: tensors must be 16-byte aligned");
+  return hip_status(pk::launch_silu_and_mul(x, x_row_stride, rows, inter, out, out_row_stride,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                    "silu_and_mul launch");
+}
+
+int pk_lm_head_greedy(const void* hidden_states, int64_t row_stride, const int32_t* cu_seqlens_q,
+                      const void* weight, int64_t weight_row_stride, int32_t rows, int32_t vocab,
+                      int32_t hidden, uint64_t* keys, int32_t* token_ids, pk_stream_t stream) {
+  g_last_error.clear();
+  if (rows < 0 || vocab <= 0) return fail(PK_ERR_INVALID_ARG, "lm_head_greedy: rows=%d, vocab=%d", rows, vocab);
+  if (rows == 0) return PK_OK;
+  if (hidden <= 0 || hidden % 128 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "lm_head_greedy: hidden=%d must be a positive multiple of 128", hidden);
+  if (!hidden_states || !weight || !keys || !token_ids)
+    return fail(PK_ERR_INVALID_ARG, "lm_head_greedy: null pointer argument");
+  if (row_stride < hidden || row_stride % 8 || weight_row_stride < hidden || weight_row_stride % 8)
+    return fail(PK_ERR_INVALID_ARG, "lm_head_greedy: row strides must be >= hidden and multiples of 8");
+  if (!aligned16(hidden_states) || !aligned16(weight) || (reinterpret_cast<uintptr_t>(keys) & 7u))
+    return fail(PK_ERR_INVALID_ARG, "lm_head_greedy: hidden_states / weight 16-byte, keys 8-byte aligned");
+  return hip_status(pk::launch_lm_head_greedy(hidden_states, row_stride, cu_seqlens_q, weight,
+                                              weight_row_stride, rows, vocab, hidden,
+                                              reinterpret_cast<unsigned long long*>(keys), token_ids,
+                                              reinterpret_cast<hipStream_t>(stream)),
+                    "lm_head_greedy launch");
 }
 
 }  // extern "C"

@@ -109,4 +109,15 @@ hipError_t launch_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride,
                                      int64_t k_out_row_stride, void* k_cache, void* v_cache,
                                      const int32_t* slot_mapping, int64_t num_slots,
                                      hipStream_t stream);
+// Residual add + RMSNorm, SiLU * mul and the greedy LM head of the serving loop.
+hipError_t launch_add_rmsnorm(const void* x, int64_t x_stride, const void* residual,
+                              int64_t res_stride, const void* weight, float eps, int32_t rows,
+                              int32_t hidden, void* out, int64_t out_stride, void* residual_out,
+                              int64_t res_out_stride, hipStream_t stream);
+hipError_t launch_silu_and_mul(const void* x, int64_t x_stride, int32_t rows, int32_t inter,
+                               void* out, int64_t out_stride, hipStream_t stream);
+hipError_t launch_lm_head_greedy(const void* x, int64_t x_stride, const int32_t* cu_rows,
+                                 const void* w, int64_t w_stride, int32_t rows, int32_t vocab,
+                                 int32_t k_dim, unsigned long long* keys, int32_t* ids,
+                                 hipStream_t stream);
 }  // namespace pk

@@ -6,12 +6,15 @@ src/utils/context.py):
     varlen_attention (flash_attn_varlen_func semantics), gather_kv,
     workspace_bytes, reserve_workspace,
     qk_norm_rope_store + rope_cos_sin (the fused q/k norm, RoPE and cache store of
-    src/models/qwen3.py:80-89).
+    src/models/qwen3.py:80-89),
+    add_rmsnorm, silu_and_mul, lm_head_greedy (the serving loop's other kernels).
 """
 from .attention import Attention, store_kvcache  # noqa: F401
 from .context import Context  # noqa: F401
-from .ops import (gather_kv, qk_norm_rope_store, reserve_workspace, rope_cos_sin,  # noqa: F401
-                  varlen_attention, workspace_bytes)
+from .ops import (add_rmsnorm, gather_kv, lm_head_greedy, qk_norm_rope_store,  # noqa: F401
+                  reserve_workspace, rope_cos_sin, silu_and_mul, varlen_attention,
+                  workspace_bytes)
 
 __all__ = ["Attention", "store_kvcache", "Context", "varlen_attention", "gather_kv",
-           "workspace_bytes", "reserve_workspace", "qk_norm_rope_store", "rope_cos_sin"]
+           "workspace_bytes", "reserve_workspace", "qk_norm_rope_store", "rope_cos_sin",
+           "add_rmsnorm", "silu_and_mul", "lm_head_greedy"]

@@ -53,9 +53,16 @@ SIGNATURES = {
         _c_void_p, _i64, _c_void_p, _i64,   # q_out, its row stride, k_out, its row stride
         _c_void_p, _c_void_p, _c_void_p,    # k_cache, v_cache, slot_mapping
         _i64, _c_void_p]),                  # num_slots, stream
+    "pk_add_rmsnorm": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _i64, _c_void_p, ctypes.c_float, _i32, _i32,
+        _c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
+    "pk_silu_and_mul": (ctypes.c_int, [_c_void_p, _i64, _i32, _i32, _c_void_p, _i64, _c_void_p]),
+    "pk_lm_head_greedy": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p,
+        _c_void_p]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -1,8 +1,10 @@
-"""Build libpagedkv.so for gfx950 from the HIP sources in ../csrc.
+"""Build libpagedkv.so for gfx950 from the HIP sources in ../csrc, and libpkhost.so (the
+host-side serving core, plain C++) from ../csrc/pkhost.cpp.
 
 Each .hip file is compiled to an object with hipcc (in parallel), then the objects
 are linked into one shared library placed next to this file, where
-``pagedkv._lib`` loads it. The build always recompiles; there is no JIT cache.
+``pagedkv._lib`` loads it; libpkhost.so is compiled with g++ and loaded by
+``pagedkv._host``. The build always recompiles; there is no JIT cache.
 
     python -m pagedkv.build          # from the nano-vllm-diy_amd directory
 """
@@ -22,6 +24,8 @@ INCLUDE = ROOT.parent / "include"
 BUILD_DIR = ROOT / "_build"
 LIB_NAME = "libpagedkv.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+HOST_LIB_PATH = PKG_DIR / "libpkhost.so"
+HOST_SRC = CSRC / "pkhost.cpp"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
@@ -59,8 +63,25 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
+def build_host(verbose: bool = False) -> Path:
+    """Compile csrc/pkhost.cpp into libpkhost.so with the host C++ compiler."""
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    tmp = HOST_LIB_PATH.with_name(HOST_LIB_PATH.name + f".tmp{os.getpid()}")
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{INCLUDE}",
+           str(HOST_SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{cxx} failed on {HOST_SRC.name}:\n{res.stderr}")
+    os.replace(tmp, HOST_LIB_PATH)
+    return HOST_LIB_PATH
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libpagedkv.so; return its path."""
+    """Compile every csrc/*.hip for gfx950 and link libpagedkv.so (and build
+    libpkhost.so); return the path of libpagedkv.so."""
+    build_host(verbose)
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")

@@ -285,3 +285,86 @@ def qk_norm_rope_store(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: torc
         ptr(k_cache), ptr(v_cache), ptr(slot_mapping), num_slots, _stream(qkv)),
         "pk_qk_norm_rope_store")
     return q_out, k_out
+
+
+def _rows2d(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 2 or t.dtype != torch.bfloat16 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D bf16 tensor with contiguous rows")
+
+
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                residual: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """RMSNorm.forward (src/layers/layernorm.py:30-39) with the residual add fused.
+
+    residual None: returns bf16(w * x * rsqrt(mean(x^2) + eps)). Otherwise returns
+    (normed, new_residual) with new_residual = bf16(x + residual), as residual_forward.
+    """
+    _rows2d("x", x)
+    rows, hidden = x.shape
+    if weight.dtype != torch.bfloat16 or weight.numel() != hidden or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous (hidden,) bf16 tensor")
+    if out is None:
+        out = torch.empty_like(x)
+    res_out = None
+    if residual is not None:
+        _rows2d("residual", residual)
+        if residual.shape != x.shape:
+            raise ValueError("residual must match x")
+        res_out = torch.empty_like(residual)
+    check(lib().pk_add_rmsnorm(
+        x.data_ptr(), x.stride(0), residual.data_ptr() if residual is not None else 0,
+        residual.stride(0) if residual is not None else 0, weight.data_ptr(), float(eps), rows,
+        hidden, out.data_ptr(), out.stride(0), res_out.data_ptr() if res_out is not None else 0,
+        res_out.stride(0) if res_out is not None else 0, _stream(x)), "pk_add_rmsnorm")
+    return out if residual is None else (out, res_out)
+
+
+def silu_and_mul(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SiluAndMul.forward (src/layers/activation.py:6-10): silu(first half) * second half."""
+    _rows2d("x", x)
+    rows, width = x.shape
+    inter = width // 2
+    if out is None:
+        out = torch.empty(rows, inter, dtype=torch.bfloat16, device=x.device)
+    check(lib().pk_silu_and_mul(x.data_ptr(), x.stride(0), rows, inter, out.data_ptr(),
+                                out.stride(0), _stream(x)), "pk_silu_and_mul")
+    return out
+
+
+_lm_keys: dict[int, torch.Tensor] = {}
+
+
+def lm_head_greedy(hidden_states: torch.Tensor, weight: torch.Tensor,
+                   cu_seqlens_q: torch.Tensor | None = None, num_rows: int | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy next tokens from ParallelLMHead.forward's logits (src/layers/llm_head.py:60-64).
+
+    With cu_seqlens_q, row m is the last token of sequence m (the prefill selection of
+    llm_head.py:61-63) and num_rows defaults to len(cu_seqlens_q) - 1; otherwise every row.
+    Returns int32 token ids: argmax over the bf16-rounded logits, lowest id on ties.
+    """
+    _rows2d("hidden_states", hidden_states)
+    _rows2d("weight", weight)
+    hidden = hidden_states.shape[1]
+    if weight.shape[1] != hidden:
+        raise ValueError("weight must be (vocab, hidden)")
+    dev = hidden_states.device
+    if cu_seqlens_q is not None:
+        _req_i32("cu_seqlens_q", cu_seqlens_q, dev)
+        rows = cu_seqlens_q.numel() - 1 if num_rows is None else num_rows
+    else:
+        rows = hidden_states.shape[0] if num_rows is None else num_rows
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    keys = _lm_keys.get(idx)
+    if keys is None or keys.numel() < rows:
+        keys = torch.empty(max(rows, 512), dtype=torch.int64, device=dev)
+        if not torch.cuda.is_current_stream_capturing():
+            _lm_keys[idx] = keys
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=dev)
+    check(lib().pk_lm_head_greedy(
+        hidden_states.data_ptr(), hidden_states.stride(0),
+        cu_seqlens_q.data_ptr() if cu_seqlens_q is not None else 0, weight.data_ptr(),
+        weight.stride(0), rows, weight.shape[0], hidden, keys.data_ptr(), out.data_ptr(),
+        _stream(hidden_states)), "pk_lm_head_greedy")
+    return out
