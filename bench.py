@@ -11,9 +11,12 @@ time, in GB/s; all inputs are resident in HBM before the timed region starts.
 `roofline` is the decode attention call alone, timed per launch with HIP events on
 the stream it is launched on. `cpu_baseline` is the CPU oracle (torch on all host
 cores) on a bounded sample of the same workload. `kernels` reports every other
-configuration (store, mixed chunked prefill + decode, shared-prefix decode).
+configuration (store, mixed chunked prefill + decode, shared-prefix decode, the fused
+q/k norm + RoPE + store producer). `e2e` is the serving configuration: offline continuous
+batching of 256 requests on a random-init Qwen3-0.6B-geometry model (greedy, ignore_eos),
+output tokens per second of generate() (the reference's bench.py:67-72 formula).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline] [--no-e2e]
 """
 from __future__ import annotations
 
@@ -154,10 +157,13 @@ def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configurations")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end serving run")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the end-to-end serving run (prints its JSON object), for profiling")
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU-baseline sample")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 cfg2 decode calls and 5 copies of 1 GiB (the counter calibration), "
@@ -175,6 +181,9 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.e2e_only:
+        print(json.dumps(run_e2e(dev)), flush=True)
+        return 0
     log("[bench] building cfg2 (256 seqs, Lk ~ U[1024, 8192]) on the GPU")
     w = make_workload("cfg2", dev)
     if args.pmc_probe:
@@ -262,6 +271,11 @@ def main() -> int:
     del w
     torch.cuda.empty_cache()
 
+    if not args.no_e2e:
+        log("[bench] e2e: 256 requests on a random-init Qwen3-0.6B")
+        result["e2e"] = run_e2e(dev)
+        torch.cuda.empty_cache()
+
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle on host cores)")
         wc = make_workload("cfg2", dev)
@@ -269,6 +283,43 @@ def main() -> int:
         del wc
     print(json.dumps(result), flush=True)
     return 0
+
+
+def run_e2e(dev, seed: int = 5) -> dict:
+    """Offline continuous batching, the serving configuration: 256 requests, prompt ids
+    U[0, 151936), prompt and output lengths U[100, 1024], ignore_eos, greedy, block 256,
+    16384-token budget. The timed region is generate() (requests added inside it, as in the
+    reference's bench.py:67-72); model init and graph capture are outside."""
+    import random
+
+    import torch
+
+    from pagedkv.engine import LLMEngine
+    from pagedkv.qwen3 import Qwen3Config
+
+    cfg = Qwen3Config()
+    t0 = time.perf_counter()
+    eng = LLMEngine(cfg, device=dev, num_blocks=2048, block_size=256,
+                    max_num_batched_tokens=16384, seed=seed)
+    torch.cuda.synchronize()
+    init_s = time.perf_counter() - t0
+    rng = random.Random(seed)
+    prompts = [[rng.randrange(cfg.vocab_size) for _ in range(rng.randint(100, 1024))]
+               for _ in range(256)]
+    max_tokens = [rng.randint(100, 1024) for _ in range(256)]
+    outs, st = eng.generate(prompts, max_tokens, ignore_eos=True)
+    assert [len(o) for o in outs] == max_tokens
+    res = {"tok_per_s": round(st.tok_per_s, 1), "output_tokens": st.output_tokens,
+           "wall_s": round(st.wall_s, 3), "steps": st.steps, "decode_steps": st.decode_steps,
+           "prefill_steps": st.prefill_steps, "prefill_tokens": st.prefill_tokens,
+           "init_and_capture_s": round(init_s, 2),
+           "workload": "256 requests, prompt ids U[0,151936), prompt/output lengths U[100,1024], "
+                       "ignore_eos, greedy; random-init Qwen3-0.6B geometry (28 layers, hidden "
+                       "1024, 16q/8kv heads, head_dim 128, FFN 3072, vocab 151936), bf16, "
+                       "block 256, 16384-token budget, 128 live sequences"}
+    log(f"[bench] e2e {res['tok_per_s']} tok/s ({st.output_tokens} tokens in {st.wall_s:.2f} s)")
+    del eng
+    return res
 
 
 def pmc_probe(w) -> int:
