@@ -110,8 +110,9 @@ int pk_store_kvcache(const void* key, int64_t key_row_stride,
  *   out  (Nq, num_heads, head_dim) bf16, token row stride out_row_stride.
  *
  * Built for head_dim == 128, num_heads % num_kv_heads == 0 with the group
- * size in {1, 2, 4, 8}; block_size a multiple of 64 in paged mode.
- * Softmax and accumulation are fp32.
+ * size in {1, 2, 4, 8}, num_kv_heads <= 255, max_seqlen_q and max_seqlen_k up
+ * to 65535 * 64; block_size a multiple of 64 in paged mode. Softmax and
+ * accumulation are fp32.
  */
 int pk_varlen_attention(const void* q, int64_t q_row_stride,
                         const void* k, const void* v,
@@ -128,11 +129,14 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride,
                         pk_stream_t stream);
 
 /*
- * Bytes of workspace pk_varlen_attention needs for these launch bounds (the
- * split-K partial outputs of the decode kernel; 0 when every sequence fits
- * one split, in which case workspace may be NULL). No
- * counterpart in the reference: flash-attn allocates its split-K buffers
- * internally, which a graph-capturable, allocation-free ABI cannot do.
+ * Bytes of workspace pk_varlen_attention needs for these launch bounds: the
+ * split-K partial outputs of the decode kernel (none when every sequence fits
+ * one split) and, when max_seqlen_q > 1, the prefill work plan (work list,
+ * merge list and the partial outputs of query tiles split over key ranges,
+ * about 100 MB at most). 0 means workspace may be NULL. The contents need no
+ * initialisation: each call writes what it reads. No counterpart in the
+ * reference: flash-attn allocates its split-K buffers internally, which a
+ * graph-capturable, allocation-free ABI cannot do.
  */
 size_t pk_varlen_attention_workspace_bytes(int32_t num_seqs, int32_t num_heads,
                                            int32_t head_dim, int32_t max_seqlen_q,

@@ -4,6 +4,8 @@
 // alignment of every vector-loaded pointer), fills the kernel argument block and
 // enqueues on the caller's stream. Nothing here allocates, synchronises or reads
 // device memory, so every call can be recorded into a hipGraph.
+#include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -35,6 +37,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 constexpr size_t kWorkspaceAlign = 256;
 constexpr int kMaxSeqs = 65535;
+constexpr int kMaxSeqlen = 65535 * 64;  // key tiles of 64 keys fit in 16 bits
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -43,12 +46,16 @@ struct WorkspaceLayout {
   int max_splits;
   size_t part_o_bytes;
   size_t part_ml_bytes;
+  // chunked-prefill plan region (only when max_seqlen_q > 1)
+  int64_t pf_item_cap;
+  size_t pf_queue_off, pf_items_off, pf_merges_off, pf_part_o_off, pf_part_ml_off;
   size_t total;
 };
 
-// [per-split partial numerators | per-split (max, sum)]; empty when no sequence can
-// have more than one split (those write their output directly).
-WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_k) {
+// [decode: per-split partial numerators | per-split (max, sum)]  (empty when no sequence
+// can have more than one split: those write their output directly)
+// [prefill: queue header | work items | merge list | partial numerators | (max, sum)]
+WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_q, int max_seqlen_k) {
   WorkspaceLayout w{};
   w.split_tokens = pk::decode_split_tokens(num_seqs, max_seqlen_k);
   w.max_splits = max_seqlen_k > 0 ? (max_seqlen_k + w.split_tokens - 1) / w.split_tokens : 0;
@@ -57,7 +64,21 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
     w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
     w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
   }
-  w.total = w.part_o_bytes + w.part_ml_bytes;
+  size_t off = w.part_o_bytes + w.part_ml_bytes;
+  if (max_seqlen_q > 1) {
+    w.pf_item_cap = pk::prefill_item_cap(num_seqs, num_heads, max_seqlen_q);
+    w.pf_queue_off = off;
+    off += round_up(pk::kPrefillQueueInts * sizeof(int32_t), kWorkspaceAlign);
+    w.pf_items_off = off;
+    off += round_up((size_t)w.pf_item_cap * 16, kWorkspaceAlign);
+    w.pf_merges_off = off;
+    off += round_up((size_t)pk::kPrefillMergeCap * 16, kWorkspaceAlign);
+    w.pf_part_o_off = off;
+    off += (size_t)pk::kPrefillPartCap * 32 * pk::kPrefillRows * 4 * sizeof(float);
+    w.pf_part_ml_off = off;
+    off += round_up((size_t)pk::kPrefillPartCap * pk::kPrefillRows * 2 * sizeof(float), kWorkspaceAlign);
+  }
+  w.total = off;
   return w;
 }
 
@@ -120,9 +141,8 @@ int pk_gather_kv(const void* cache, int64_t block_stride, int32_t block_size,
 
 size_t pk_varlen_attention_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                            int32_t max_seqlen_q, int32_t max_seqlen_k) {
-  (void)max_seqlen_q;
-  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0) return 0;
-  return workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_k).total;
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0 || max_seqlen_q < 0) return 0;
+  return workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k).total;
 }
 
 int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, const void* v,
@@ -149,6 +169,12 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
   if (num_seqs == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) return PK_OK;
   if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k)
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: null pointer argument");
+  // the prefill work list packs key-tile indices in 16 bits and the kv head in 8
+  if (max_seqlen_k > kMaxSeqlen || max_seqlen_q > kMaxSeqlen)
+    return fail(PK_ERR_UNSUPPORTED, "varlen_attention: max_seqlen_q=%d / max_seqlen_k=%d above %d",
+                max_seqlen_q, max_seqlen_k, kMaxSeqlen);
+  if (num_kv_heads > 255)
+    return fail(PK_ERR_UNSUPPORTED, "varlen_attention: num_kv_heads=%d above 255", num_kv_heads);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: q/k/v/out must be 16-byte aligned");
   const int64_t kv_row = (int64_t)num_kv_heads * head_dim;
@@ -176,7 +202,7 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
   if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: softmax_scale must be positive and finite");
 
-  const WorkspaceLayout ws = workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_k);
+  const WorkspaceLayout ws = workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k);
   if (ws.total > 0) {
     if (!workspace || workspace_bytes < ws.total)
       return fail(PK_ERR_WORKSPACE, "varlen_attention: workspace of %zu bytes needed, %zu given",
@@ -184,6 +210,10 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
     if ((reinterpret_cast<uintptr_t>(workspace) % kWorkspaceAlign) != 0)
       return fail(PK_ERR_WORKSPACE, "varlen_attention: workspace must be %zu-byte aligned", kWorkspaceAlign);
   }
+
+  if (max_seqlen_q > 1 && ws.pf_item_cap > INT32_MAX)
+    return fail(PK_ERR_UNSUPPORTED, "varlen_attention: prefill work list of %lld items too large",
+                (long long)ws.pf_item_cap);
 
   pk::AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
@@ -208,9 +238,20 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
   a.out_row_stride = out_row_stride;
   a.split_tokens = ws.split_tokens;
   a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
-  if (ws.total > 0) {
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.part_o_bytes);
+  char* const wsb = static_cast<char*>(workspace);
+  if (ws.part_o_bytes > 0) {
+    a.part_o = reinterpret_cast<float*>(wsb);
+    a.part_ml = reinterpret_cast<float*>(wsb + ws.part_o_bytes);
+  }
+  if (max_seqlen_q > 1) {
+    a.pf_queue = reinterpret_cast<int32_t*>(wsb + ws.pf_queue_off);
+    a.pf_items = reinterpret_cast<int4*>(wsb + ws.pf_items_off);
+    a.pf_merges = reinterpret_cast<int4*>(wsb + ws.pf_merges_off);
+    a.pf_part_o = reinterpret_cast<float*>(wsb + ws.pf_part_o_off);
+    a.pf_part_ml = reinterpret_cast<float*>(wsb + ws.pf_part_ml_off);
+    a.pf_item_cap = (int32_t)std::min<int64_t>(ws.pf_item_cap, INT32_MAX);
+    a.pf_merge_cap = pk::kPrefillMergeCap;
+    a.pf_part_cap = pk::kPrefillPartCap;
   }
 
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);

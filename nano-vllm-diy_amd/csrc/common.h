@@ -44,7 +44,37 @@ struct AttnArgs {
   float* part_ml;               // [num_seqs][max_splits][num_heads][2] = (max, sum)
   int32_t split_tokens;
   int32_t max_splits;
+  // chunked-prefill work plan (workspace): a work item is (sequence, kv head, query tile,
+  // key-tile range); items of one query tile that was split over several key ranges write
+  // fp32 partials that a merge pass combines.
+  int32_t* pf_queue;            // kPrefillQueueInts header: 8 claim counters, item / merge counts
+  int4* pf_items;               // [pf_item_cap] groups (b, qt, tile_begin | tile_end << 16, partial group);
+                                // item i = kv head i % Hkv of group i / Hkv
+  int4* pf_merges;              // [pf_merge_cap] split units (b, qt, first partial group, splits)
+  float* pf_part_o;             // [part][32 chunks of 4 dims][kPrefillRows][4] unnormalised numerators
+  float* pf_part_ml;            // [part][kPrefillRows][2] = (running max in the exp2 domain, sum)
+  int32_t pf_item_cap;
+  int32_t pf_merge_cap;
+  int32_t pf_part_cap;
+  int32_t pf_slots;             // persistent work-groups of the prefill kernel
+  int32_t prefill_qtiles;       // upper bound on query tiles per sequence (from max_seqlen_q)
 };
+
+// Prefill plan sizes. The kernel runs kPrefillSlotsMax persistent work-groups at most (one
+// per CU on a 256-CU part). The split size T is at least 2/3 x total work / slots, and
+// every split unit has more than T tiles, so its n splits satisfy n < 2 t / T: fewer than
+// 3 x slots partials (all kv heads) ever exist, in fewer than 1.5 x slots split units.
+constexpr int kPrefillSlotsMax = 256;
+constexpr int kPrefillQueueInts = 64;   // header ints (256 bytes)
+constexpr int kPrefillRows = 256;       // query rows per work item (query tokens x GQA heads)
+constexpr int kPrefillPartCap = 3 * kPrefillSlotsMax;
+constexpr int kPrefillMergeCap = 3 * kPrefillSlotsMax / 2;
+// Groups: one per (sequence, query tile) plus the extra splits (fewer than partials).
+// Query tiles per sequence are at most ceil(Lq * G / 256) <= ceil(Lq * Hq / 256).
+inline int64_t prefill_item_cap(int num_seqs, int num_heads, int max_seqlen_q) {
+  return (int64_t)num_seqs * (((int64_t)max_seqlen_q * num_heads + kPrefillRows - 1) / kPrefillRows) +
+         kPrefillPartCap;
+}
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

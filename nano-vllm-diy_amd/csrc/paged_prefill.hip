@@ -7,39 +7,89 @@
 // Keys come through the block table (paged, chunked prefill / prefix-cache hits) or
 // from fresh rows at cu_seqlens_k (flat, all-fresh prompts).
 //
-// Work decomposition: grid = (query tile, kv head g, sequence). A work-group of four
-// wavefronts owns 128 query rows = TM = 128 / G query tokens x the G query heads of kv
-// head g, so each K/V tile staged in LDS serves the whole GQA group. Wavefront w owns
-// 32 rows (one head, 32 consecutive tokens, or 2 heads x 16 tokens when G = 8).
+// Work unit: 256 query rows = TM = 256 / G query tokens x the G query heads of one kv
+// head g, so each K/V tile staged in LDS serves the whole GQA group. A work-group of eight
+// wavefronts (two per SIMD, one work-group per CU) owns the unit; wavefront w owns rows
+// 32 w .. 32 w + 31, which are 32 consecutive tokens of one head (TM >= 32 for every GQA
+// group built). The two wavefronts of a SIMD run the same loop out of phase, so one's
+// softmax overlaps the other's MFMAs.
 //
-// Per tile of TN = 32 keys (per wavefront):
-//   S^T (32 keys x 32 rows)  = K (32 x 128) . Q^T (128 x 32)   8 v_mfma_f32_32x32x16_bf16
-//   online softmax down each column (a lane owns one query row: 16 scores in registers,
-//   one xor-32 exchange for the column max)
-//   O^T (128 x 32)          += V^T (128 x 32) . P^T (32 x 32)  4 x 2 v_mfma_f32_32x32x16_bf16
-// K is staged row-major in LDS; V is staged transposed (d-major) so that the MFMA A
-// operand (8 keys of one d) is two 8-byte LDS reads. P^T never leaves registers: the
-// S^T accumulator layout already holds, per lane, the keys the P.V B operand needs
-// once the k-order of the instruction is permuted (same permutation on the V^T side).
+// Three launches, all sized on the host without reading device memory:
+//   1. plan (one work-group): reads cu_seqlens_q/k, counts each unit's key tiles under
+//      its causal limit, picks a split size of max(8, total tiles / pool) tiles and writes
+//      the work list: every unit longer than the split size is cut into equal key ranges.
+//      Long items come first (a two-bucket longest-first order).
+//   2. prefill (a persistent pool of one work-group per CU): each work-group claims items
+//      from the sub-queue of its XCD (item i belongs to sub-queue i mod 8, which for 8 kv
+//      heads is kv head i mod 8, so a head's K/V stays in one XCD's L2), then steals from
+//      the other sub-queues. An unsplit item writes bf16 rows; a split item writes its
+//      fp32 numerators and (max, sum) per row.
+//   3. merge: combines the partials of every split unit.
+// The split bounds the longest chain of dependent tiles (a long cached prefix would
+// otherwise keep one work-group busy long after the rest of the GPU has finished).
+//
+// Per 64-key tile, per wavefront and 32-row block:
+//   S^T (64 keys x 32 rows) = K (64 x 128) . Q^T (128 x 32)    16 v_mfma_f32_32x32x16_bf16
+//   online softmax down each column (a lane owns one query row; the two lane halves
+//   exchange through v_permlane32_swap)
+//   O^T (128 x 32)         += V^T (128 x 64) . P^T (64 x 32)   16 v_mfma_f32_32x32x16_bf16
+// K and V are staged row-major in a four-stage LDS ring (128 KiB) filled by DMA three tiles
+// ahead;
+// the P.V A operand comes from the LDS transpose read. P^T never leaves registers: the
+// S^T accumulator layout already holds, per lane, the keys the P.V B operand needs once
+// the k-order of the instruction is permuted (same permutation on the V side).
+#include <algorithm>
+
 #include "common.h"
 
 namespace pk {
 namespace {
 
-constexpr int kTileKeys = 64;        // keys per K/V tile
-constexpr int kPrefillThreads = 256;  // four wavefronts
-constexpr int kRowBytes = kHeadDim * 2;                  // one head's row of a K or V tile (256 B)
-constexpr int kTileBytes = kTileKeys * kRowBytes;        // 16 KiB per operand per buffer
-
-#ifndef PK_PREFILL_WAVES_PER_SIMD
-#define PK_PREFILL_WAVES_PER_SIMD 2  // register budget: 512 / this per lane (VGPR + AGPR)
+constexpr int kTileKeys = 64;          // keys per K/V tile
+#ifndef PK_PREFILL_ROW_BLOCKS
+#define PK_PREFILL_ROW_BLOCKS 1
 #endif
+// A wavefront owns kRowBlocks blocks of 32 query rows; every K and V operand it reads from
+// LDS serves all of its blocks, so LDS read traffic per flop falls as 1 / kRowBlocks.
+constexpr int kRowBlocks = PK_PREFILL_ROW_BLOCKS;
+static_assert(kRowBlocks == 1 || kRowBlocks == 2, "row blocks per wavefront");
+constexpr int kPrefillWaves = 8 / kRowBlocks;           // 256 rows per work-group
+constexpr int kPrefillThreads = kPrefillWaves * 64;
+constexpr int kWavesPerSimd = 2 / kRowBlocks;           // register file: 512 / this per lane
+constexpr int kRowBytes = kHeadDim * 2;                  // one head's row of a K or V tile (256 B)
+constexpr int kTileBytes = kTileKeys * kRowBytes;        // 16 KiB per operand per stage
+constexpr int kPlanThreads = 1024;     // plan work-group
+constexpr int kPlanCache = 2048;       // sequences whose lengths the plan keeps in LDS
+constexpr int kMinSplitTiles = 8;      // never split a unit's keys below 512 per item
+constexpr int kMergeThreads = 256;     // merge: thread = row of the unit
+constexpr int kMergeGroups = 1024;
+constexpr int kBuckets = 4;            // length buckets of the work list (longest first)
+constexpr float kLazyLog2 = 8.f;       // reference max moves only when exceeded by 2^8
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value of lane l ^ 32 (the other half of the wavefront), one VALU swap.
+__device__ __forceinline__ float swap_halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float swap_halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
+// Work-group barrier for the LDS tiles: wait until this wavefront's LDS instructions have
+// completed, then s_barrier. It is issued as an instruction of its own because
+// __syncthreads() would also wait for every global load in flight (its fence waits for
+// vmcnt(0)), including the next tile's loads that are meant to overlap the compute.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt((15 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0) only
+  asm volatile("s_barrier" ::: "memory");
+}
 
 // LDS tiles are stored unpadded, one 256-byte row per key, with the row's sixteen 16-byte
 // chunks XOR-swizzled so that the MFMA operand reads hit distinct banks:
@@ -48,20 +98,52 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((2 * r) & 15); }
 
-// Global -> LDS for keys [t0, t0 + 64) of kv head g straight into `kdst` / `vdst` with
-// global_load_lds_dwordx4: wavefront w moves rows 16 w .. 16 w + 15, four rows (1 KiB) per
-// instruction, lane l writing slot (l & 15) of row (l >> 4) and therefore reading the
-// swizzled source chunk. No registers hold tile data. Keys past Lk re-read the last key's
-// row (same cache block, finite data); their scores are masked and their p is 0.
+// Keys [t0, t0 + 64) of kv head g move global -> registers -> LDS: wavefront w owns tile
+// rows kRowsPerWave w .. kRowsPerWave (w + 1) - 1, four rows (1 KiB) per 16-byte load
+// instruction, lane l carrying slot (l & 15) of row (l >> 4) and therefore the swizzled
+// source chunk. The loads for tile n + 2 are issued before tile n is computed and written
+// to LDS after tile n + 1 has been (register staging keeps them off the LDS while it
+// serves the MFMA operands). Keys past Lk re-read the last key's row (same cache block,
+// finite data); their scores are masked and their p is 0.
+constexpr int kRowsPerWave = kTileKeys / kPrefillWaves;
+constexpr int kLoadsPerOperand = kRowsPerWave / 4;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Per-lane source offsets (elements) of the rows this lane moves.
+struct LoadLanes {
+  int k[kLoadsPerOperand];
+  int v[kLoadsPerOperand];
+};
+
+__device__ __forceinline__ LoadLanes load_lanes(const AttnArgs& a, int wave, int lane, int last) {
+  LoadLanes l;
+  const int slot = lane & 15;
+#pragma unroll
+  for (int i = 0; i < kLoadsPerOperand; ++i) {
+    const int r = kRowsPerWave * wave + 4 * i + (lane >> 4);  // tile row this lane fills
+    const int rs = min(r, last);                              // source row (clamped on the last tile)
+    l.k[i] = rs * (int)a.k_row_stride + (slot ^ (r & 15)) * 8;
+    l.v[i] = rs * (int)a.v_row_stride + (slot ^ ((2 * r) & 15)) * 8;
+  }
+  return l;
+}
+
+struct KvRegs {
+  u32x4 k[kLoadsPerOperand];
+  u32x4 v[kLoadsPerOperand];
+};
+
 template <bool PAGED>
-__device__ __forceinline__ void load_tile_lds(const AttnArgs& a, int b, int k0, int Lk, int g, int bt_lane, int wave,
-                                              int lane, int t0, lds_char* kdst, lds_char* vdst) {
+__device__ __forceinline__ void load_tile_regs(const AttnArgs& a, int b, int k0, int Lk, int g, int bt_lane, int wave,
+                                               int lane, int t0, const LoadLanes& full_lanes, KvRegs& R) {
   const uint16_t* kbase;
   const uint16_t* vbase;
   if constexpr (PAGED) {
     const int j = t0 / a.block_size;  // block_size % 64 == 0: the tile sits inside one block
     const int blk = j < kWave ? __builtin_amdgcn_readlane(bt_lane, j)
-                              : a.block_table[(int64_t)b * a.bt_stride + j];
+                              : __builtin_amdgcn_readfirstlane(a.block_table[(int64_t)b * a.bt_stride + j]);
     const int off = t0 % a.block_size;
     kbase = a.k + (int64_t)blk * a.k_block_stride + (int64_t)off * a.k_row_stride;
     vbase = a.v + (int64_t)blk * a.v_block_stride + (int64_t)off * a.v_row_stride;
@@ -71,159 +153,346 @@ __device__ __forceinline__ void load_tile_lds(const AttnArgs& a, int b, int k0, 
   }
   kbase += g * kHeadDim;
   vbase += g * kHeadDim;
-  const int last = Lk - 1 - t0;
-  const int slot = lane & 15;
+  const LoadLanes l = (t0 + kTileKeys <= Lk) ? full_lanes : load_lanes(a, wave, lane, Lk - 1 - t0);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * wave + 4 * i + (lane >> 4);  // tile row this lane fills
-    const int rs = min(r, last);                    // source row
-    const uint16_t* ksrc = kbase + (int64_t)rs * a.k_row_stride + (slot ^ (r & 15)) * 8;
-    const uint16_t* vsrc = vbase + (int64_t)rs * a.v_row_stride + (slot ^ ((2 * r) & 15)) * 8;
-    __builtin_amdgcn_global_load_lds(ksrc, kdst + (16 * wave + 4 * i) * kRowBytes, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vsrc, vdst + (16 * wave + 4 * i) * kRowBytes, 16, 0, 0);
+  for (int i = 0; i < kLoadsPerOperand; ++i) {
+    R.k[i] = *reinterpret_cast<const u32x4*>(kbase + l.k[i]);
+    R.v[i] = *reinterpret_cast<const u32x4*>(vbase + l.v[i]);
   }
 }
 
-// One key tile for this wavefront's 32 query rows:
-//   S^T = K Q^T, online softmax down the columns, O^T += V^T P^T.
-// full: no key of the tile is masked for any row of the wavefront (wave-uniform).
-__device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char* sV, const bf16x8 (&qb)[kHeadDim / 16],
-                                             f32x16 (&o)[4], float& m_i, float& l_i, int t0, int lim, bool full,
-                                             float scale_log2, int lane) {
-  const int col = lane & 31;
-  const int half = lane >> 5;
-  // S^T accumulator element rr of half-tile mb is key t0 + 32 mb + 8 (rr >> 2) + 4 half + (rr & 3).
-  // A operand: lane (col, half) needs chunk 2 kb + half of K row 32 mb + col.
-  f32x16 s[2];
+__device__ __forceinline__ void store_tile_lds(const KvRegs& R, lds_char* kdst, lds_char* vdst, int wave, int lane) {
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int i = 0; i < kLoadsPerOperand; ++i) {
+    const int off = (kRowsPerWave * wave + 4 * i) * kRowBytes + lane * 16;
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(kdst + off) = R.k[i];
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(vdst + off) = R.v[i];
+  }
+}
+
+// Online softmax of one 32-row block's S^T tile (64 keys) in place: scores become p, the
+// row sums move on, and p is packed to bf16 as the P.V B operand. S^T element rr of
+// half-tile mb is key t0 + 32 mb + 8 (rr >> 2) + 4 half + (rr & 3). Raw scores are
+// compared (the scale is positive) and scaled inside the exponent's FMA.
+// Lazy rescaling: exponentials are taken against a reference max m_i (exp2 domain) that
+// moves only when some row's tile max exceeds it by more than kLazyLog2; then every row
+// moves to its running max and the numerator and sum are rescaled. p <= 2^kLazyLog2, and
+// numerator and sum share the reference, so o / l is unchanged.
+__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf16x8 (&pb)[4], float& m_i, float& l_i,
+                                              int t0, int lim, bool full, float scale_log2, int half) {
+  if (!full) {
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) s[mb][rr] = 0.f;
-    const int r = mb * 32 + col;
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-    for (int kb = 0; kb < kHeadDim / 16; ++kb) {
-      const bf16x8 av = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(
-          sK + r * kRowBytes + k_slot(r, 2 * kb + half) * 16);
-      s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qb[kb], s[mb], 0, 0, 0);
-    }
+      for (int rr = 0; rr < 16; ++rr)
+        if (t0 + mb * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3) > lim) s[mb][rr] = -INFINITY;
   }
   float tmax = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      float v = s[mb][rr] * scale_log2;
-      if (!full && t0 + mb * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3) > lim) v = -INFINITY;
-      s[mb][rr] = v;
-      tmax = fmaxf(tmax, v);
-    }
-  tmax = fmaxf(tmax, xor_shfl(tmax, 32));
-  const float m_new = fmaxf(m_i, tmax);
-  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;  // row saw no key yet
-  const float alpha = exp2_fast(m_i - m_use);
-  m_i = m_new;
-  float psum = 0.f;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const float p = exp2_fast(s[mb][rr] - m_use);
-      s[mb][rr] = p;
-      psum += p;
-    }
-  l_i = l_i * alpha + psum;
-  // rescale the numerator only when some row of the wavefront raised its max (rare once
-  // the running max has settled)
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+    for (int rr = 0; rr < 16; ++rr) tmax = fmaxf(tmax, s[mb][rr]);
+  const float tm = swap_halves_max(tmax) * scale_log2;
+  if (__builtin_amdgcn_ballot_w64(tm > m_i + kLazyLog2) != 0) {
+    const float m_new = fmaxf(m_i, tm);
+    const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_i - m_new);  // 0 when m_i = -inf
+    m_i = m_new;
+    l_i *= alpha;
 #pragma unroll
     for (int md = 0; md < 4; ++md)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) o[md][rr] *= alpha;
   }
-  // O^T += V^T . P^T over 16-key k-blocks. The instruction pairs A and B by (lane half,
-  // element e); element e of half `half` stands for key 16 kb2 + 8 (e >> 2) + 4 half +
-  // (e & 3), which is accumulator element 8 (kb2 & 1) + e of S^T half-tile kb2 >> 1.
-  // The A operand (4 consecutive keys of one head_dim element, twice) comes from the
-  // row-major V tile through the LDS transpose read: in each 16-lane group, source lane
-  // s addresses 4 elements of key row key0 + (s >> 2) at head_dim d0 + 4 (s & 3), and
-  // lane i receives element d0 + i of keys key0 .. key0 + 3.
+  const float m_use = (m_i == -INFINITY) ? 0.f : m_i;  // row saw no key yet: every p is 0
+  float psum = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const float p = exp2_fast(__builtin_fmaf(s[mb][rr], scale_log2, -m_use));
+      s[mb][rr] = p;
+      psum += p;
+    }
+  l_i += psum;
+  // B operand of k-block kb2: element e of lane half `half` stands for key
+  // 16 kb2 + 8 (e >> 2) + 4 half + (e & 3) = accumulator element 8 (kb2 & 1) + e of
+  // half-tile kb2 >> 1.
+#pragma unroll
+  for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pb[kb2][e] = static_cast<__bf16>(s[kb2 >> 1][8 * (kb2 & 1) + e]);
+}
+
+// Per-lane LDS byte offsets of the MFMA operand reads inside a stage.
+//   K, k-block kb: row col (+ 32 for the second half-tile: + 8 KiB), chunk 2 kb + half,
+//     swizzled with col & 15 (32 mb + col has the same low bits);
+//   V, d-block md: row 4 half + (src >> 2) (+ 16 kb2 rows: + 4 KiB, + 8 rows: + 2 KiB), the
+//     swizzle (2 r) & 15 does not see those row steps.
+struct TileLanes {
+  int k[kHeadDim / 16];
+  int v[4];
+};
+
+__device__ __forceinline__ TileLanes tile_lanes(int lane) {
+  TileLanes t;
+  const int col = lane & 31;
+  const int half = lane >> 5;
   const int grp = lane >> 4;
   const int src = lane & 15;
 #pragma unroll
-  for (int kb2 = 0; kb2 < 4; ++kb2) {
-    bf16x8 pb;
+  for (int kb = 0; kb < kHeadDim / 16; ++kb) t.k[kb] = col * kRowBytes + k_slot(col, 2 * kb + half) * 16;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pb[e] = static_cast<__bf16>(s[kb2 >> 1][8 * (kb2 & 1) + e]);
+  for (int md = 0; md < 4; ++md) {
+    const int d = md * 32 + 16 * (grp & 1) + 4 * (src & 3);
+    const int r = 4 * half + (src >> 2);
+    t.v[md] = r * kRowBytes + v_slot(r, d >> 3) * 16 + (d & 7) * 2;
+  }
+  return t;
+}
+
+// One 64-key tile for the wavefront's kRowBlocks blocks of 32 query rows.
+__device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char* sV, const TileLanes& tl,
+                                             const bf16x8 (&qb)[kRowBlocks][kHeadDim / 16],
+                                             f32x16 (&o)[kRowBlocks][4], float (&m_i)[kRowBlocks],
+                                             float (&l_i)[kRowBlocks], int t0, const int (&lim)[kRowBlocks],
+                                             const bool (&full)[kRowBlocks], float scale_log2, int lane) {
+  const int half = lane >> 5;
+  f32x16 s[kRowBlocks][2];
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; ++rb)
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) s[rb][mb][rr] = 0.f;
+  // K A operand of half-tile mb, k-block kb, read in batches of kKBatch k-blocks (both
+  // half-tiles) ahead of their MFMAs.
+  constexpr int kKBatch = kRowBlocks == 1 ? kHeadDim / 16 : kHeadDim / 32;
+#pragma unroll
+  for (int k0b = 0; k0b < kHeadDim / 16; k0b += kKBatch) {
+    bf16x8 ka[2][kKBatch];
+#pragma unroll
+    for (int kk = 0; kk < kKBatch; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        ka[mb][kk] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(sK + tl.k[k0b + kk] +
+                                                                                     mb * 32 * kRowBytes);
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb)
+#pragma unroll
+      for (int kk = 0; kk < kKBatch; ++kk)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+          s[rb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[mb][kk], qb[rb][k0b + kk], s[rb][mb], 0, 0, 0);
+  }
+
+  bf16x8 pb[kRowBlocks][4];
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; ++rb)
+    softmax_block(s[rb], o[rb], pb[rb], m_i[rb], l_i[rb], t0, lim[rb], full[rb], scale_log2, half);
+
+  // O^T += V^T . P^T over 16-key k-blocks. The A operand (4 consecutive keys of one
+  // head_dim element, twice) comes from the row-major V tile through the LDS transpose
+  // read: in each 16-lane group, source lane s addresses 4 elements of key row
+  // key0 + (s >> 2) at head_dim d0 + 4 (s & 3), and lane i receives element d0 + i of keys
+  // key0 .. key0 + 3. Each A operand serves every row block.
+#pragma unroll
+  for (int kb2 = 0; kb2 < 4; ++kb2) {
 #pragma unroll
     for (int md = 0; md < 4; ++md) {
-      const int d = md * 32 + 16 * (grp & 1) + 4 * (src & 3);
-      const int r_lo = 16 * kb2 + 4 * half + (src >> 2);
-      const int r_hi = r_lo + 8;
-      const lds_v4i16* p_lo = reinterpret_cast<const lds_v4i16*>(sV + r_lo * kRowBytes + v_slot(r_lo, d >> 3) * 16 + (d & 7) * 2);
-      const lds_v4i16* p_hi = reinterpret_cast<const lds_v4i16*>(sV + r_hi * kRowBytes + v_slot(r_hi, d >> 3) * 16 + (d & 7) * 2);
-      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(p_lo));
-      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_v4i16*>(p_hi));
+      const lds_char* p_lo = sV + tl.v[md] + kb2 * 16 * kRowBytes;
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          const_cast<lds_v4i16*>(reinterpret_cast<const lds_v4i16*>(p_lo)));
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          const_cast<lds_v4i16*>(reinterpret_cast<const lds_v4i16*>(p_lo + 8 * kRowBytes)));
       const bf16x8 av = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb, o[md], 0, 0, 0);
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb)
+        o[rb][md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[rb][kb2], o[rb][md], 0, 0, 0);
     }
   }
 }
 
-template <int G, bool PAGED, bool CAUSAL>
-__global__ __launch_bounds__(kPrefillThreads, PK_PREFILL_WAVES_PER_SIMD) void prefill_kernel(const AttnArgs a) {
-  constexpr int D = kHeadDim;
-  constexpr int TN = kTileKeys;
-  constexpr int TM = 128 / G;  // query tokens per work-group
-  // two buffers per operand, as distinct objects so the compiler can tell the tile being
-  // filled by the DMA apart from the tile being read
-  __shared__ __attribute__((aligned(1024))) char sK0[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sV0[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sK1[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sV1[kTileBytes];
-  lds_char* const K0 = (lds_char*)sK0;  // address-space cast to LDS
-  lds_char* const V0 = (lds_char*)sV0;
-  lds_char* const K1 = (lds_char*)sK1;
-  lds_char* const V1 = (lds_char*)sV1;
+// Sequence geometry shared by the plan, prefill and merge kernels.
+struct SeqDims {
+  int q0, Lq, k0, Lk, P, nq;  // nq: query tiles of the sequence (0: not a prefill sequence)
+};
 
+template <int TM>
+__device__ __forceinline__ SeqDims seq_dims(const AttnArgs& a, int b) {
+  SeqDims d;
+  d.q0 = a.cu_q[b];
+  d.Lq = a.cu_q[b + 1] - d.q0;
+  d.k0 = a.cu_k[b];
+  d.Lk = min(a.cu_k[b + 1] - d.k0, a.max_seqlen_k);
+  d.P = d.Lk - d.Lq;
+  // Lq == 1 rows belong to the decode kernel; Lq <= 0 or Lk <= 0 is graph padding
+  d.nq = (d.Lq <= 1 || d.Lk <= 0) ? 0 : min((d.Lq + TM - 1) / TM, a.prefill_qtiles);
+  return d;
+}
+
+// Key tiles query tile qt needs: keys below its last row's causal limit.
+template <int TM, bool CAUSAL>
+__device__ __forceinline__ int unit_tiles(const SeqDims& d, int qt) {
+  const int kv_end = CAUSAL ? min(d.Lk, (qt + 1) * TM + d.P) : d.Lk;
+  return kv_end > 0 ? (kv_end + kTileKeys - 1) / kTileKeys : 0;
+}
+
+// Splits of a unit of t tiles for split size T, and the start tile of split s.
+__device__ __forceinline__ int unit_splits(int t, int T) { return t > T ? (t + T - 1) / T : 1; }
+__device__ __forceinline__ int split_begin(int t, int n, int s) { return (int)((unsigned)(t * s) / (unsigned)n); }
+
+// Length bucket of a group of t tiles (0 = longest) for split size T.
+__device__ __forceinline__ int length_bucket(int t, int T) {
+  return t * kBuckets > (kBuckets - 1) * T ? 0 : t * kBuckets > (kBuckets - 2) * T ? 1 : t * kBuckets > T ? 2 : 3;
+}
+
+// Work list. Waves take sequences in turn and lanes take a sequence's query tiles, so a
+// long prompt's tiles are planned in parallel. Groups land in their length bucket through
+// LDS cursors: the order inside a bucket depends on timing, but a group's work and the
+// merge order of its splits do not, so results are bit-identical from run to run.
+template <int G, bool CAUSAL>
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const AttnArgs a) {
+  constexpr int TM = kPrefillRows / G;
+  constexpr int W = kPlanThreads / kWave;
+  __shared__ long long red[W];
+  __shared__ int cur[kBuckets + 2];  // bucket cursors, partial-group cursor, merge cursor
+  // (Lq, Lk) of up to kPlanCache sequences, so passes 2 and 3 skip the global round trip
+  __shared__ int2 dims[kPlanCache];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int qt = blockIdx.x;
-  const int g = blockIdx.y;
-  const int b = blockIdx.z;
+  const int wave = tid / kWave;
+  const int S = a.num_seqs;
+  const int hkv = a.num_kv_heads;
 
-  const int q0 = a.cu_q[b];
-  const int Lq = a.cu_q[b + 1] - q0;
-  if (Lq <= 1) return;  // Lq == 1 rows belong to the decode kernel; Lq <= 0 is padding
-  const int k0 = a.cu_k[b];
-  const int Lk = min(a.cu_k[b + 1] - k0, a.max_seqlen_k);
-  if (Lk <= 0) return;
-  const int tok_begin = qt * TM;
-  if (tok_begin >= Lq) return;
-  const int P = Lk - Lq;  // cached prefix length
-  int kv_end = Lk;
-  if (CAUSAL) kv_end = min(Lk, tok_begin + TM + P);  // keys any row of this tile can see
+  for (int b = tid; b < min(S, kPlanCache); b += kPlanThreads) {
+    const SeqDims d = seq_dims<TM>(a, b);
+    dims[b] = make_int2(d.Lq, d.Lk);
+  }
+  __syncthreads();
+  auto dims_of = [&](int b) {
+    if (b >= kPlanCache) return seq_dims<TM>(a, b);
+    SeqDims d;
+    d.q0 = d.k0 = 0;  // not used by the plan
+    d.Lq = dims[b].x;
+    d.Lk = dims[b].y;
+    d.P = d.Lk - d.Lq;
+    d.nq = (d.Lq <= 1 || d.Lk <= 0) ? 0 : min((d.Lq + TM - 1) / TM, a.prefill_qtiles);
+    return d;
+  };
 
-  const int col = lane & 31;   // MFMA column = this lane's query row
-  const int half = lane >> 5;
-  const int row = wave * 32 + col;
-  const int h = g * G + row / TM;
-  const int tok = tok_begin + row % TM;
-  const bool row_valid = tok < Lq;
-  const int lim = CAUSAL ? min(Lk - 1, tok + P) : Lk - 1;  // last key this row sees
-  // the wavefront's rows are tokens [w_lo, w_lo + min(32, TM)) of one or two heads
-  const int w_lo = tok_begin + (wave * 32) % TM;
-  const int w_hi = w_lo + (TM < 32 ? TM : 32) - 1;
-  const int lim_lo = CAUSAL ? min(Lk - 1, w_lo + P) : Lk - 1;  // keys <= lim_lo: seen by all rows
-  const int lim_hi = CAUSAL ? min(Lk - 1, w_hi + P) : Lk - 1;  // keys >  lim_hi: seen by none
-
-  // Q^T B operand: k-block kb covers d in [16 kb, 16 kb + 16); lane holds 8 of them.
-  // Rows past Lq read the last row (finite) and are never stored.
-  bf16x8 qb[D / 16];
-  {
-    const uint16_t* qp = a.q + (int64_t)(q0 + min(tok, Lq - 1)) * a.q_row_stride + h * D + 8 * half;
+  // pass 1: total key tiles over all units
+  long long tiles = 0;
+  for (int b = wave; b < S; b += W) {
+    const SeqDims d = dims_of(b);
+    for (int qt = lane; qt < d.nq; qt += kWave) tiles += unit_tiles<TM, CAUSAL>(d, qt);
+  }
 #pragma unroll
-    for (int kb = 0; kb < D / 16; ++kb) qb[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + kb * 16));
+  for (int o = kWave / 2; o > 0; o >>= 1) tiles += __shfl_xor(tiles, o, kWave);
+  if (lane == 0) red[wave] = tiles;
+  if (tid < kBuckets + 2) cur[tid] = 0;
+  __syncthreads();
+  long long work = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) work += red[w];
+  work *= hkv;
+  // split size: 1.5 groups of work per slot, at least kMinSplitTiles (no unit has 2^20 tiles)
+  const int T = (int)min((long long)(1 << 20),
+                         max((long long)kMinSplitTiles, (2 * (work / 3) + a.pf_slots - 1) / a.pf_slots + 1));
+
+  // pass 2: groups per length bucket
+  for (int b = wave; b < S; b += W) {
+    const SeqDims d = dims_of(b);
+    for (int qt = lane; qt < d.nq; qt += kWave) {
+      const int t = unit_tiles<TM, CAUSAL>(d, qt);
+      const int n = unit_splits(t, T);
+      for (int sp = 0; sp < n; ++sp)
+        atomicAdd(&cur[length_bucket(split_begin(t, n, sp + 1) - split_begin(t, n, sp), T)], 1);
+    }
+  }
+  __syncthreads();
+  int tot = 0, start[kBuckets];
+#pragma unroll
+  for (int k = 0; k < kBuckets; ++k) {
+    start[k] = tot;
+    tot += cur[k];
+  }
+  __syncthreads();
+  if (tid < kBuckets) cur[tid] = 0;
+  __syncthreads();
+
+  // pass 3: emit one entry per group; kv heads are expanded by index (item i = head i % hkv
+  // of group i / hkv)
+  for (int b = wave; b < S; b += W) {
+    const SeqDims d = dims_of(b);
+    for (int qt = lane; qt < d.nq; qt += kWave) {
+      const int t = unit_tiles<TM, CAUSAL>(d, qt);
+      const int n = unit_splits(t, T);
+      // partial groups stay below 3 x slots / hkv (each split unit has more than T tiles)
+      const int pg = n > 1 ? atomicAdd(&cur[kBuckets], n) : -1;
+      for (int sp = 0; sp < n; ++sp) {
+        const int tb = split_begin(t, n, sp);
+        const int te = split_begin(t, n, sp + 1);
+        const int k = length_bucket(te - tb, T);
+        const int grp = start[k] + atomicAdd(&cur[k], 1);
+        if (grp < a.pf_item_cap) a.pf_items[grp] = make_int4(b, qt, tb | (te << 16), n > 1 ? pg + sp : -1);
+      }
+      if (n > 1) {
+        const int m = atomicAdd(&cur[kBuckets + 1], 1);
+        if (m < a.pf_merge_cap) a.pf_merges[m] = make_int4(b, qt, pg, n);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 8) a.pf_queue[tid] = 0;
+  if (tid == 0) {
+    a.pf_queue[8] = (int)(min((int64_t)tot, (int64_t)a.pf_item_cap) * hkv);
+    a.pf_queue[9] = (int)(min((int64_t)cur[kBuckets + 1], (int64_t)a.pf_merge_cap) * hkv);
+    a.pf_queue[10] = T;
+  }
+}
+
+// One work item: kv head g of group `it` = (sequence b, query tile qt, key tiles [tb, te),
+// partial group or -1).
+template <int G, bool PAGED, bool CAUSAL>
+__device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, const int g, lds_char* const (&KS)[2],
+                                             lds_char* const (&VS)[2], int wave, int lane) {
+  constexpr int D = kHeadDim;
+  constexpr int TN = kTileKeys;
+  constexpr int TM = kPrefillRows / G;
+  static_assert(TM >= 32, "a 32-row block is one head");
+  const int b = it.x;
+  const int qt = it.y;
+  const int tb = it.z & 0xffff;
+  const int te = it.z >> 16;
+  const int part = it.w < 0 ? -1 : it.w * a.num_kv_heads + g;
+  const SeqDims sd = seq_dims<TM>(a, b);
+  const int q0 = sd.q0, Lq = sd.Lq, k0 = sd.k0, Lk = sd.Lk, P = sd.P;
+  const int tok_begin = qt * TM;
+
+  const int col = lane & 31;   // MFMA column = this lane's query row inside a block
+  const int half = lane >> 5;
+  int row[kRowBlocks], h[kRowBlocks], tok[kRowBlocks], lim[kRowBlocks], lim_lo[kRowBlocks], lim_hi[kRowBlocks];
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; ++rb) {
+    const int r0 = (wave * kRowBlocks + rb) * 32;  // first row of the block: 32 tokens of one head
+    row[rb] = r0 + col;
+    h[rb] = g * G + row[rb] / TM;
+    tok[rb] = tok_begin + row[rb] % TM;
+    lim[rb] = CAUSAL ? min(Lk - 1, tok[rb] + P) : Lk - 1;  // last key this row sees
+    const int blo = tok_begin + r0 % TM;
+    lim_lo[rb] = CAUSAL ? min(Lk - 1, blo + P) : Lk - 1;       // keys <= lim_lo: seen by all rows
+    lim_hi[rb] = CAUSAL ? min(Lk - 1, blo + 31 + P) : Lk - 1;  // keys >  lim_hi: seen by none
+  }
+
+  // Q^T B operands: k-block kb covers d in [16 kb, 16 kb + 16); lane holds 8 of them.
+  // Rows past Lq read the last row (finite) and are never stored.
+  bf16x8 qb[kRowBlocks][D / 16];
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; ++rb) {
+    const uint16_t* qp = a.q + (int64_t)(q0 + min(tok[rb], Lq - 1)) * a.q_row_stride + h[rb] * D + 8 * half;
+#pragma unroll
+    for (int kb = 0; kb < D / 16; ++kb)
+      qb[rb][kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + kb * 16));
   }
   // The sequence's first 64 block-table entries sit one per lane in a register, so a tile's
   // block id is a readlane instead of a dependent global load.
@@ -233,71 +502,240 @@ __global__ __launch_bounds__(kPrefillThreads, PK_PREFILL_WAVES_PER_SIMD) void pr
     if (lane < nblk) bt_lane = a.block_table[(int64_t)b * a.bt_stride + lane];
   }
 
-  f32x16 o[4];
+  f32x16 o[kRowBlocks][4];
+  float m_i[kRowBlocks], l_i[kRowBlocks];
 #pragma unroll
-  for (int md = 0; md < 4; ++md)
+  for (int rb = 0; rb < kRowBlocks; ++rb) {
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) o[md][rr] = 0.f;
-  float m_i = -INFINITY;
-  float l_i = 0.f;
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) o[rb][md][rr] = 0.f;
+    m_i[rb] = -INFINITY;
+    l_i[rb] = 0.f;
+  }
 
-  // Pipeline (one barrier per tile): after the barrier, tile n is complete in LDS and no
-  // wavefront still reads the other buffer, so tile n+1 is sent there by DMA while tile n
-  // is computed; the wavefront then waits for its own DMA, and the next barrier publishes
-  // it. Tiles entirely above a wavefront's causal limit are skipped by that wavefront.
-  const int ntiles = (kv_end + TN - 1) / TN;
-  if (ntiles > 0) load_tile_lds<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, 0, K0, V0);
-  __builtin_amdgcn_s_waitcnt(0);  // Q operand, block table and tile 0 have landed
-  __syncthreads();
-  for (int n = 0; n < ntiles; n += 2) {
-    const int t0 = n * TN;
-    if (n + 1 < ntiles) load_tile_lds<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, t0 + TN, K1, V1);
-    if (t0 <= lim_hi) compute_tile(K0, V0, qb, o, m_i, l_i, t0, lim, t0 + TN - 1 <= lim_lo, a.scale_log2, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (n + 1 >= ntiles) break;
-    const int t1 = t0 + TN;
-    if (n + 2 < ntiles) load_tile_lds<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, t1 + TN, K0, V0);
-    if (t1 <= lim_hi) compute_tile(K1, V1, qb, o, m_i, l_i, t1, lim, t1 + TN - 1 <= lim_lo, a.scale_log2, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  // Pipeline, one barrier per tile: at step n, the loads of tile n + 2 go out, tile n is
+  // computed from stage n & 1, tile n + 1 (registers) is written to stage (n + 1) & 1 -- last
+  // read at step n - 1, before the previous barrier -- and the barrier publishes it.
+  const int ntiles = te - tb;
+  const int tbase = tb * TN;
+  const LoadLanes ll = load_lanes(a, wave, lane, kTileKeys);
+  const TileLanes tl = tile_lanes(lane);
+  KvRegs R;
+  if (ntiles > 0) {
+    load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, tbase, ll, R);
+    store_tile_lds(R, KS[0], VS[0], wave, lane);
+  }
+  if (ntiles > 1) load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, tbase + TN, ll, R);
+  lds_barrier();
+  for (int n0 = 0; n0 < ntiles; n0 += 2) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int n = n0 + s;
+      if (n >= ntiles) break;
+      const int t0 = tbase + n * TN;
+      KvRegs Rn;
+      if (n + 2 < ntiles) load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, t0 + 2 * TN, ll, Rn);
+      bool any = false, full[kRowBlocks];
+#pragma unroll
+      for (int rb = 0; rb < kRowBlocks; ++rb) {
+        any |= t0 <= lim_hi[rb];
+        full[rb] = t0 + TN - 1 <= lim_lo[rb];
+      }
+      if (any) compute_tile(KS[s], VS[s], tl, qb, o, m_i, l_i, t0, lim, full, a.scale_log2, lane);
+      if (n + 1 < ntiles) store_tile_lds(R, KS[s ^ 1], VS[s ^ 1], wave, lane);
+      lds_barrier();
+      R = Rn;
+    }
   }
 
   // Epilogue: O^T element rr of d-block md is d = 32 md + 8 (rr >> 2) + 4 half + (rr & 3).
-  const float l_tot = l_i + xor_shfl(l_i, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // a row that saw no key is written as 0
-  if (!row_valid) return;
-  uint16_t* op = a.out + (int64_t)(q0 + tok) * a.out_row_stride + h * D + 4 * half;
 #pragma unroll
-  for (int md = 0; md < 4; ++md)
+  for (int rb = 0; rb < kRowBlocks; ++rb) {
+    const float l_tot = swap_halves_sum(l_i[rb]);
+    if (tok[rb] >= Lq) continue;
+    if (part < 0) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // a row that saw no key is written as 0
+      uint16_t* op = a.out + (int64_t)(q0 + tok[rb]) * a.out_row_stride + h[rb] * D + 4 * half;
 #pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      uint2 w;
-      w.x = pack_bf16x2(o[md][4 * grp] * inv, o[md][4 * grp + 1] * inv);
-      w.y = pack_bf16x2(o[md][4 * grp + 2] * inv, o[md][4 * grp + 3] * inv);
-      *reinterpret_cast<uint2*>(op + md * 32 + 8 * grp) = w;
+      for (int md = 0; md < 4; ++md)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          uint2 w;
+          w.x = pack_bf16x2(o[rb][md][4 * gq] * inv, o[rb][md][4 * gq + 1] * inv);
+          w.y = pack_bf16x2(o[rb][md][4 * gq + 2] * inv, o[rb][md][4 * gq + 3] * inv);
+          *reinterpret_cast<uint2*>(op + md * 32 + 8 * gq) = w;
+        }
+    } else if (part < a.pf_part_cap) {
+      // numerators chunk-major (chunk = 4 dims = d / 4), so one store instruction writes two
+      // contiguous 512-byte runs (32 rows x 16 bytes per lane half)
+      float* po = a.pf_part_o + (int64_t)part * (32 * kPrefillRows * 4);
+#pragma unroll
+      for (int md = 0; md < 4; ++md)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int chunk = 8 * md + 2 * gq + half;
+          const float4 w = make_float4(o[rb][md][4 * gq], o[rb][md][4 * gq + 1], o[rb][md][4 * gq + 2],
+                                       o[rb][md][4 * gq + 3]);
+          *reinterpret_cast<float4*>(po + ((int64_t)chunk * kPrefillRows + row[rb]) * 4) = w;
+        }
+      if (half == 0)
+        *reinterpret_cast<float2*>(a.pf_part_ml + ((int64_t)part * kPrefillRows + row[rb]) * 2) =
+            make_float2(m_i[rb], l_tot);
     }
+  }
+}
+
+template <int G, bool PAGED, bool CAUSAL>
+__global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel(const AttnArgs a) {
+  // two stages per operand (constant stage indices put the stage offset in immediates)
+  __shared__ __attribute__((aligned(1024))) char sK[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sV[2][kTileBytes];
+  __shared__ int s_item[2];  // alternating claim slots: one barrier per claim
+  lds_char* KS[2];
+  lds_char* VS[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    KS[st] = (lds_char*)sK[st];
+    VS[st] = (lds_char*)sV[st];
+  }
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  // Work-groups are dealt to the 8 XCDs round-robin by linear id: this one serves sub-queue
+  // blockIdx mod 8 first (items i = 8 j + x), then the others in turn. Every claim moves a
+  // counter forward, and a work-group leaves once all eight sub-queues are exhausted.
+  const int xcd = blockIdx.x & 7;
+  const int num_items = a.pf_queue[8];
+  int sq = 0;
+  for (int it = 0;; it ^= 1) {
+    if (tid == 0) {
+      int idx = -1;
+      while (sq < 8) {
+        const int q = (xcd + sq) & 7;
+        const int64_t cand = (int64_t)atomicAdd(&a.pf_queue[q], 1) * 8 + q;
+        if (cand < num_items) {
+          idx = (int)cand;
+          break;
+        }
+        ++sq;
+      }
+      s_item[it] = idx;
+    }
+    // Slot `it` is rewritten two claims later, after the next claim's barrier, which every
+    // wavefront passes only once it has read this one. Pending stores of the previous item
+    // need not drain here.
+    lds_barrier();
+    const int idx = __builtin_amdgcn_readfirstlane(s_item[it]);
+    if (idx < 0) break;
+    const int grp = idx / a.num_kv_heads;
+    prefill_item<G, PAGED, CAUSAL>(a, a.pf_items[grp], idx - grp * a.num_kv_heads, KS, VS, wave, lane);
+  }
+}
+
+// Merge the partials of every split unit: out = sum_s w_s o_s / sum_s w_s l_s with
+// w_s = exp2(m_s - max_s m_s). Work item = (split unit, quarter of head_dim, kv head);
+// thread t owns row t of the unit and 8 chunks of 4 dims.
+// At most 4 wavefronts per SIMD: the register budget lets all of a split's loads be in
+// flight at once instead of one 16-byte load per memory latency.
+template <int G>
+__global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void prefill_merge_kernel(
+    const AttnArgs a) {
+  constexpr int D = kHeadDim;
+  constexpr int TM = kPrefillRows / G;
+  constexpr int CQ = 8;  // chunks per quarter
+  const int nw = a.pf_queue[9] * 4;
+  const int r = threadIdx.x;
+  const int hkv = a.num_kv_heads;
+  // w = (unit, quarter) * hkv + g: with 8 kv heads, head g's merges run on XCD g (work-groups
+  // go to XCDs round-robin and the grid is a multiple of 8), where the prefill kernel's
+  // sub-queue g wrote its partials, so the reads mostly hit that XCD's L2
+  for (int w = blockIdx.x; w < nw; w += gridDim.x) {
+    const int rest = w / hkv;
+    const int g = w - rest * hkv;
+    const int c0 = (rest & 3) * CQ;
+    const int unit = rest >> 2;
+    const int4 e = a.pf_merges[unit];
+    const int b = e.x;
+    const int qt = e.y;
+    const int pg = e.z;
+    const int n = e.w;
+    const int q0 = a.cu_q[b];
+    const int Lq = a.cu_q[b + 1] - q0;
+    const int tok = qt * TM + r % TM;
+    const int h = g * G + r / TM;
+    if (tok >= Lq) continue;
+    if ((pg + n) * hkv > a.pf_part_cap) continue;  // cannot happen: the plan bounds partial ids
+    // two passes over the splits: running max, then weights and numerators; every pass
+    // issues all of a split's loads before using them
+    float M = -INFINITY;
+    for (int s = 0; s < n; ++s) M = fmaxf(M, a.pf_part_ml[((int64_t)((pg + s) * hkv + g) * kPrefillRows + r) * 2]);
+    float4 acc[CQ];
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.f;
+    if (M != -INFINITY) {
+      for (int s = 0; s < n; ++s) {
+        const int p = (pg + s) * hkv + g;
+        const float* po = a.pf_part_o + (int64_t)p * (32 * kPrefillRows * 4);
+        f32x4 v[CQ];
+#pragma unroll
+        for (int c = 0; c < CQ; ++c) v[c] = *reinterpret_cast<const f32x4*>(po + ((int64_t)(c0 + c) * kPrefillRows + r) * 4);
+        const float2 ml = *reinterpret_cast<const float2*>(a.pf_part_ml + ((int64_t)p * kPrefillRows + r) * 2);
+        const float wgt = exp2_fast(ml.x - M);  // 0 for a split whose rows saw no key
+        L += wgt * ml.y;
+#pragma unroll
+        for (int c = 0; c < CQ; ++c) {
+          acc[c].x += wgt * v[c][0];
+          acc[c].y += wgt * v[c][1];
+          acc[c].z += wgt * v[c][2];
+          acc[c].w += wgt * v[c][3];
+        }
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint16_t* op = a.out + (int64_t)(q0 + tok) * a.out_row_stride + h * D + 4 * c0;
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) {
+      uint2 wv;
+      wv.x = pack_bf16x2(acc[c].x * inv, acc[c].y * inv);
+      wv.y = pack_bf16x2(acc[c].z * inv, acc[c].w * inv);
+      *reinterpret_cast<uint2*>(op + 4 * c) = wv;
+    }
+  }
+}
+
+int device_prefill_slots() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kPrefillSlotsMax;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = kPrefillSlotsMax;
+    cached[dev] = std::min(cus, kPrefillSlotsMax);  // one work-group per CU
+  }
+  return cached[dev];
+}
+
+template <int G, bool PAGED, bool CAUSAL>
+hipError_t launch_prefill_gpc(const AttnArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((prefill_plan_kernel<G, CAUSAL>), dim3(1), dim3(kPlanThreads), 0, stream, a);
+  hipLaunchKernelGGL((prefill_kernel<G, PAGED, CAUSAL>), dim3(a.pf_slots), dim3(kPrefillThreads), 0, stream, a);
+  hipLaunchKernelGGL((prefill_merge_kernel<G>), dim3(kMergeGroups), dim3(kMergeThreads), 0, stream, a);
+  return hipGetLastError();
 }
 
 template <int G>
-hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_seqlen_q,
-                            hipStream_t stream) {
-  constexpr int TM = 128 / G;
-  const dim3 grid((unsigned)((max_seqlen_q + TM - 1) / TM), (unsigned)a.num_kv_heads,
-                  (unsigned)a.num_seqs);
-  const dim3 block(kPrefillThreads);
-  if (paged) {
-    if (causal)
-      hipLaunchKernelGGL((prefill_kernel<G, true, true>), grid, block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((prefill_kernel<G, true, false>), grid, block, 0, stream, a);
-  } else {
-    if (causal)
-      hipLaunchKernelGGL((prefill_kernel<G, false, true>), grid, block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((prefill_kernel<G, false, false>), grid, block, 0, stream, a);
-  }
-  return hipGetLastError();
+hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_seqlen_q, hipStream_t stream) {
+  constexpr int TM = kPrefillRows / G;
+  AttnArgs pa = a;
+  pa.prefill_qtiles = (max_seqlen_q + TM - 1) / TM;
+  pa.pf_slots = device_prefill_slots();
+  if (paged)
+    return causal ? launch_prefill_gpc<G, true, true>(pa, stream) : launch_prefill_gpc<G, true, false>(pa, stream);
+  return causal ? launch_prefill_gpc<G, false, true>(pa, stream) : launch_prefill_gpc<G, false, false>(pa, stream);
 }
 
 }  // namespace
@@ -305,6 +743,7 @@ hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_
 hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal, int max_seqlen_q,
                           hipStream_t stream) {
   if (a.num_seqs <= 0 || max_seqlen_q <= 1) return hipSuccess;
+  if (!a.pf_queue || !a.pf_items || !a.pf_merges || !a.pf_part_o || !a.pf_part_ml) return hipErrorInvalidValue;
   switch (group) {
     case 1: return launch_prefill_g<1>(a, paged, causal, max_seqlen_q, stream);
     case 2: return launch_prefill_g<2>(a, paged, causal, max_seqlen_q, stream);
