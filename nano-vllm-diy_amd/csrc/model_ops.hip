@@ -228,6 +228,141 @@ __global__ __launch_bounds__(kLmThreads, 2) void lm_head_greedy_kernel(
   }
 }
 
+// Resident variant for hidden <= kLmResidentMaxK: a persistent work-group (one per CU) keeps
+// its group of up to 64 hidden rows in LDS for the whole call and walks vocabulary tiles,
+// so the hidden rows cross from L2 once per work-group instead of once per tile. The
+// `groups` work-groups that cover the row groups of one vocabulary sequence have linear
+// ids l, l + 8, ... and so sit on one XCD: each weight tile comes from HBM once and is
+// shared through that XCD's L2.
+constexpr int kLmResidentMaxK = 1024;
+constexpr int kLmResidentRows = 64;
+constexpr int kLmResidentWaves = 8;
+constexpr int kLmResidentThreads = kLmResidentWaves * 64;
+constexpr int kLmResidentTile = kLmResidentWaves * 32;  // vocabulary rows per tile
+
+template <int RT>
+__global__ __launch_bounds__(kLmResidentThreads, 1) void lm_head_resident_kernel(
+    const uint16_t* __restrict__ x, int64_t x_stride, const int32_t* __restrict__ cu_rows,
+    const uint16_t* __restrict__ w, int64_t w_stride, int32_t rows, int32_t vocab, int32_t k_dim,
+    int32_t groups, unsigned long long* __restrict__ keys) {
+  constexpr int MT = 32 * RT;
+  constexpr int kRowElems = kLmResidentMaxK + 8;  // staged row with a 16-byte pad
+  __shared__ __attribute__((aligned(16))) uint16_t xs[MT * kRowElems];
+  __shared__ unsigned long long best_s[kLmResidentWaves][MT];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int r = lane & 31, h = lane >> 5;
+  const int j = blockIdx.x >> 3;
+  const int rg = j % groups;                          // row group
+  const int rank = (j / groups) * 8 + (blockIdx.x & 7);  // position in the vocabulary walk
+  const int nrank = gridDim.x / groups;
+  const int m0 = rg * MT;
+
+  // stage the group's hidden rows (the last row of sequence m when selecting,
+  // llm_head.py:61-63; padded sequences and rows past `rows` stage zeros)
+  const int pieces = k_dim / 8;
+  for (int p = threadIdx.x; p < MT * pieces; p += kLmResidentThreads) {
+    const int row = p / pieces, piece = p - row * pieces;
+    const int m = m0 + row;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (m < rows) {
+      const int src = cu_rows != nullptr ? cu_rows[m + 1] - 1 : m;
+      if (src >= 0) val = *reinterpret_cast<const uint4*>(x + (int64_t)src * x_stride + piece * 8);
+    }
+    *reinterpret_cast<uint4*>(xs + row * kRowElems + piece * 8) = val;
+  }
+  __syncthreads();
+
+  unsigned long long best[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) best[t] = 0;
+  // One stream of (tile, chunk) steps: the weight chunk of step n + 2 is in flight while
+  // step n runs, across tile boundaries too.
+  const int ntiles = (vocab + kLmResidentTile - 1) / kLmResidentTile;
+  const int nchunks = k_dim / kLmKChunk;
+  const int my_tiles = rank < ntiles ? (ntiles - rank + nrank - 1) / nrank : 0;
+  const int steps = my_tiles * nchunks;
+  auto wchunk = [&](int step) {
+    const int t = step / nchunks;
+    const int c = step - t * nchunks;
+    const int v_row = (rank + t * nrank) * kLmResidentTile + wave * 32 + r;
+    return w + (int64_t)(v_row < vocab ? v_row : vocab - 1) * w_stride + 64 * h + c * kLmKChunk;
+  };
+  f32x16 acc[RT];
+  auto run_step = [&](const uint4 (&a)[8], int step) {
+    const int t = step / nchunks;
+    const int c = step - t * nchunks;
+    if (c == 0) {
+#pragma unroll
+      for (int q = 0; q < RT; ++q)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[q][i] = 0.f;
+    }
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a[s8]);
+#pragma unroll
+      for (int q = 0; q < RT; ++q) {
+        const uint4 bw = *reinterpret_cast<const uint4*>(xs + (32 * q + r) * kRowElems + c * kLmKChunk + 64 * h + 8 * s8);
+        acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8_t, bw), acc[q], 0, 0, 0);
+      }
+    }
+    if (c == nchunks - 1) {
+      // D layout: lane holds column (hidden row) 32 q + r and vocab rows 8 (i >> 2) + 4 h + (i & 3)
+      const int v_base = (rank + t * nrank) * kLmResidentTile + wave * 32;
+#pragma unroll
+      for (int q = 0; q < RT; ++q)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int v = v_base + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (v < vocab) {
+            const unsigned long long key = logit_key(round_to_bf16(acc[q][i]), (uint32_t)v);
+            best[q] = key > best[q] ? key : best[q];
+          }
+        }
+    }
+  };
+  uint4 a0[8], a1[8];
+  if (steps > 0) {
+    const uint16_t* p0 = wchunk(0);
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) a0[s8] = *reinterpret_cast<const uint4*>(p0 + 8 * s8);
+  }
+  if (steps > 1) {
+    const uint16_t* p1 = wchunk(1);
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) a1[s8] = *reinterpret_cast<const uint4*>(p1 + 8 * s8);
+  }
+  for (int step = 0; step < steps; step += 2) {
+    run_step(a0, step);
+    if (step + 2 < steps) {
+      const uint16_t* pn = wchunk(step + 2);
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) a0[s8] = *reinterpret_cast<const uint4*>(pn + 8 * s8);
+    }
+    if (step + 1 >= steps) break;
+    run_step(a1, step + 1);
+    if (step + 3 < steps) {
+      const uint16_t* pn = wchunk(step + 3);
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) a1[s8] = *reinterpret_cast<const uint4*>(pn + 8 * s8);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const unsigned long long other = __shfl_xor(best[t], 32, kWave);
+    const unsigned long long b = other > best[t] ? other : best[t];
+    if (h == 0) best_s[wave][32 * t + r] = b;
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < MT; q += kLmResidentThreads) {
+    unsigned long long b = best_s[0][q];
+#pragma unroll
+    for (int wv = 1; wv < kLmResidentWaves; ++wv) b = best_s[wv][q] > b ? best_s[wv][q] : b;
+    if (m0 + q < rows) atomicMax(keys + m0 + q, b);
+  }
+}
+
 __global__ void lm_keys_clear_kernel(unsigned long long* keys, int32_t rows) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < rows) keys[i] = 0ull;
@@ -283,7 +418,23 @@ hipError_t launch_lm_head_greedy(const void* x, int64_t x_stride, const int32_t*
   const unsigned vt = (unsigned)((vocab + kLmVocabTile - 1) / kLmVocabTile);
   auto* xp = static_cast<const uint16_t*>(x);
   auto* wp = static_cast<const uint16_t*>(w);
-  if (rows <= 32) {
+  if (k_dim <= kLmResidentMaxK) {
+    static int cus_cached = 0;
+    if (cus_cached == 0) {
+      int dev = 0, cus = 0;
+      if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+      cus_cached = cus;
+    }
+    const int groups = (rows + kLmResidentRows - 1) / kLmResidentRows;
+    const int per = 8 * groups;                      // one XCD round of every row group
+    int grid = (cus_cached / per) * per;
+    if (grid == 0) grid = per;
+    if (rows <= 32)
+      hipLaunchKernelGGL(lm_head_resident_kernel<1>, dim3(grid), dim3(kLmResidentThreads), 0, stream, xp, x_stride, cu_rows, wp, w_stride, rows, vocab, k_dim, groups, keys);
+    else
+      hipLaunchKernelGGL(lm_head_resident_kernel<2>, dim3(grid), dim3(kLmResidentThreads), 0, stream, xp, x_stride, cu_rows, wp, w_stride, rows, vocab, k_dim, groups, keys);
+  } else if (rows <= 32) {
     hipLaunchKernelGGL(lm_head_greedy_kernel<1>, dim3(vt, 1), dim3(kLmThreads), 0, stream, xp, x_stride, cu_rows, wp, w_stride, rows, vocab, k_dim, keys);
   } else if (rows <= 64) {
     hipLaunchKernelGGL(lm_head_greedy_kernel<2>, dim3(vt, 1), dim3(kLmThreads), 0, stream, xp, x_stride, cu_rows, wp, w_stride, rows, vocab, k_dim, keys);
