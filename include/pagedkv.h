@@ -229,6 +229,45 @@ int pk_lm_head_greedy(const void* hidden_states, int64_t row_stride, const int32
                       const void* weight, int64_t weight_row_stride, int32_t rows, int32_t vocab,
                       int32_t hidden, uint64_t* keys, int32_t* token_ids, pk_stream_t stream);
 
+/*
+ * Decode-step linear layers: y = x W^T for at most 128 token rows (the serving loop's decode
+ * batches), bf16 operands with fp32 accumulation, the output rounded to bf16 before the
+ * operation that follows it (as F.linear's bf16 result is in the reference), and that
+ * operation fused. They replace the F.linear calls of Qwen3Attention / Qwen3MLP
+ * (src/models/qwen3.py:80, :90, :120, :122 through ColumnParallelLinear.forward and
+ * RowParallelLinear.forward, src/layers/linear.py:74-75, :169-170) together with the op
+ * after them (SiluAndMul at qwen3.py:121; the decoder layer's RMSNorms at qwen3.py:165, :167).
+ * x (rows, k), weight (rows_w, k) row-major, n_out a multiple of 32, k a multiple of 256;
+ * every pointer 16-byte aligned, row strides multiples of 8 elements; out must not overlap x.
+ * rows > 128 returns PK_ERR_UNSUPPORTED (larger batches belong to a library GEMM).
+ * workspace: pk_linear_workspace_bytes(rows, n_out, k, epilogue) bytes (may be 0), 16-byte
+ * aligned; its contents are not needed before or after a call. Calls that share a
+ * workspace must not overlap.
+ *
+ * pk_linear -- epilogue PK_LINEAR_STORE: out = bf16(x W^T), W = weight (n_out rows).
+ *   epilogue PK_LINEAR_SILU_MUL: weight holds 2 n_out rows (gate rows, then up rows, the
+ *   MergedColumnParallelLinear layout) and out[r, c] = bf16(silu(g) * u) with
+ *   g = bf16(x . gate[c]), u = bf16(x . up[c]) (SiluAndMul, src/layers/activation.py:6-10,
+ *   computed in fp32 and rounded once).
+ * pk_linear_add_rmsnorm -- h = bf16(x W^T) (hidden = n_out columns, at most 4096), then
+ *   RMSNorm.residual_forward (src/layers/layernorm.py:18-28): s = h + residual in fp32,
+ *   out = bf16(norm_weight * (s * rsqrt(mean(s^2) + eps))), residual_out = bf16(s).
+ *   out and residual_out may alias residual.
+ */
+#define PK_LINEAR_STORE 0
+#define PK_LINEAR_SILU_MUL 1
+#define PK_LINEAR_ADD_RMSNORM 2
+
+size_t pk_linear_workspace_bytes(int32_t rows, int32_t n_out, int32_t k, int32_t epilogue);
+int pk_linear(const void* x, int64_t x_row_stride, const void* weight, int64_t weight_row_stride,
+              int32_t rows, int32_t n_out, int32_t k, int32_t epilogue, void* out, int64_t out_row_stride,
+              void* workspace, size_t workspace_bytes, pk_stream_t stream);
+int pk_linear_add_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, int64_t weight_row_stride,
+                          int32_t rows, int32_t hidden, int32_t k, const void* residual,
+                          int64_t residual_row_stride, const void* norm_weight, float eps, void* out,
+                          int64_t out_row_stride, void* residual_out, int64_t residual_out_row_stride,
+                          void* workspace, size_t workspace_bytes, pk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

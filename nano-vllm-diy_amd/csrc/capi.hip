@@ -82,11 +82,40 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
   return w;
 }
 
+// Shared argument checks of the decode-step linear entry points; 0 when valid.
+int check_linear(const char* what, const void* x, int64_t x_row_stride, const void* weight,
+                 int64_t weight_row_stride, int32_t rows, int32_t n_out, int32_t k,
+                 const void* out, int64_t out_row_stride, void* workspace, size_t workspace_bytes,
+                 size_t need) {
+  if (rows < 0) return fail(PK_ERR_INVALID_ARG, "%s: rows=%d < 0", what, rows);
+  if (rows > pk::kLinearMaxRows)
+    return fail(PK_ERR_UNSUPPORTED, "%s: rows=%d above %d (a decode-step kernel)", what, rows, pk::kLinearMaxRows);
+  if (n_out <= 0 || n_out % 32 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "%s: n_out=%d must be a positive multiple of 32", what, n_out);
+  if (k <= 0 || k % 256 != 0) return fail(PK_ERR_UNSUPPORTED, "%s: k=%d must be a positive multiple of 256", what, k);
+  if (!x || !weight || !out) return fail(PK_ERR_INVALID_ARG, "%s: null x / weight / out", what);
+  if (x_row_stride < k || x_row_stride % 8 || weight_row_stride < k || weight_row_stride % 8 ||
+      out_row_stride < n_out || out_row_stride % 8)
+    return fail(PK_ERR_INVALID_ARG, "%s: row strides must cover their rows and be multiples of 8", what);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out))
+    return fail(PK_ERR_INVALID_ARG, "%s: x / weight / out must be 16-byte aligned", what);
+  // out is written while other work-groups still read x: the two must not overlap
+  const auto xb = reinterpret_cast<uintptr_t>(x), ob = reinterpret_cast<uintptr_t>(out);
+  const uintptr_t x_end = xb + ((uintptr_t)(rows - 1) * x_row_stride + k) * 2;
+  const uintptr_t o_end = ob + ((uintptr_t)(rows - 1) * out_row_stride + n_out) * 2;
+  if (rows > 0 && xb < o_end && ob < x_end) return fail(PK_ERR_INVALID_ARG, "%s: out overlaps x", what);
+  if (workspace_bytes < need)
+    return fail(PK_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
+  if (need && (!workspace || !aligned16(workspace)))
+    return fail(PK_ERR_WORKSPACE, "%s: workspace must be non-null and 16-byte aligned", what);
+  return PK_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int pk_abi_version(void) { return 3; }
+int pk_abi_version(void) { return 4; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -367,6 +396,54 @@ int pk_lm_head_greedy(const void* hidden_states, int64_t row_stride, const int32
                                               reinterpret_cast<unsigned long long*>(keys), token_ids,
                                               reinterpret_cast<hipStream_t>(stream)),
                     "lm_head_greedy launch");
+}
+
+size_t pk_linear_workspace_bytes(int32_t rows, int32_t n_out, int32_t k, int32_t epilogue) {
+  if (rows <= 0 || rows > pk::kLinearMaxRows || n_out <= 0 || n_out % 32 || k <= 0 || k % 256) return 0;
+  return pk::linear_workspace_bytes(rows, n_out, k, epilogue);
+}
+
+int pk_linear(const void* x, int64_t x_row_stride, const void* weight, int64_t weight_row_stride,
+              int32_t rows, int32_t n_out, int32_t k, int32_t epilogue, void* out, int64_t out_row_stride,
+              void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+  g_last_error.clear();
+  if (epilogue != PK_LINEAR_STORE && epilogue != PK_LINEAR_SILU_MUL)
+    return fail(PK_ERR_INVALID_ARG, "linear: epilogue=%d is not PK_LINEAR_STORE or PK_LINEAR_SILU_MUL", epilogue);
+  const size_t need = pk_linear_workspace_bytes(rows, n_out, k, epilogue);
+  if (int rc = check_linear("linear", x, x_row_stride, weight, weight_row_stride, rows, n_out, k, out,
+                            out_row_stride, workspace, workspace_bytes, need))
+    return rc;
+  if (rows == 0) return PK_OK;
+  return hip_status(pk::launch_linear(x, x_row_stride, weight, weight_row_stride, rows, n_out, k, epilogue, out,
+                                      out_row_stride, workspace, reinterpret_cast<hipStream_t>(stream)),
+                    "linear launch");
+}
+
+int pk_linear_add_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, int64_t weight_row_stride,
+                          int32_t rows, int32_t hidden, int32_t k, const void* residual,
+                          int64_t residual_row_stride, const void* norm_weight, float eps, void* out,
+                          int64_t out_row_stride, void* residual_out, int64_t residual_out_row_stride,
+                          void* workspace, size_t workspace_bytes, pk_stream_t stream) {
+  g_last_error.clear();
+  if (hidden > 4096) return fail(PK_ERR_UNSUPPORTED, "linear_add_rmsnorm: hidden=%d above 4096", hidden);
+  const size_t need = pk_linear_workspace_bytes(rows, hidden, k, PK_LINEAR_ADD_RMSNORM);
+  if (int rc = check_linear("linear_add_rmsnorm", x, x_row_stride, weight, weight_row_stride, rows, hidden, k, out,
+                            out_row_stride, workspace, workspace_bytes, need))
+    return rc;
+  if (!residual || !residual_out || !norm_weight)
+    return fail(PK_ERR_INVALID_ARG, "linear_add_rmsnorm: null residual / residual_out / norm_weight");
+  if (residual_row_stride < hidden || residual_row_stride % 8 || residual_out_row_stride < hidden ||
+      residual_out_row_stride % 8)
+    return fail(PK_ERR_INVALID_ARG, "linear_add_rmsnorm: residual row strides must be >= hidden and multiples of 8");
+  if (!aligned16(residual) || !aligned16(residual_out) || !aligned16(norm_weight))
+    return fail(PK_ERR_INVALID_ARG, "linear_add_rmsnorm: residual / residual_out / norm_weight must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(PK_ERR_INVALID_ARG, "linear_add_rmsnorm: eps must be >= 0");
+  if (rows == 0) return PK_OK;
+  return hip_status(pk::launch_linear_add_rmsnorm(x, x_row_stride, weight, weight_row_stride, rows, hidden, k,
+                                                  residual, residual_row_stride, norm_weight, eps, out,
+                                                  out_row_stride, residual_out, residual_out_row_stride,
+                                                  workspace, reinterpret_cast<hipStream_t>(stream)),
+                    "linear_add_rmsnorm launch");
 }
 
 }  // extern "C"

@@ -146,6 +146,20 @@ hipError_t launch_add_rmsnorm(const void* x, int64_t x_stride, const void* resid
                               int64_t res_out_stride, hipStream_t stream);
 hipError_t launch_silu_and_mul(const void* x, int64_t x_stride, int32_t rows, int32_t inter,
                                void* out, int64_t out_stride, hipStream_t stream);
+// Decode-step linear layers (at most 128 rows) with fused epilogues.
+constexpr int kLinearStore = 0;       // y = bf16(x W^T)
+constexpr int kLinearSiluMul = 1;     // y = bf16(silu(g) * u) of the merged gate / up weight
+constexpr int kLinearAddRmsNorm = 2;  // residual add + RMSNorm of bf16(x W^T)
+constexpr int kLinearMaxRows = 128;
+size_t linear_workspace_bytes(int32_t rows, int32_t n_out, int32_t k, int32_t epilogue);
+hipError_t launch_linear(const void* x, int64_t x_stride, const void* w, int64_t w_stride, int32_t rows,
+                         int32_t n_out, int32_t k, int32_t epilogue, void* y, int64_t y_stride, void* ws,
+                         hipStream_t stream);
+hipError_t launch_linear_add_rmsnorm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                                     int32_t rows, int32_t n_out, int32_t k, const void* residual,
+                                     int64_t res_stride, const void* norm_weight, float eps, void* out,
+                                     int64_t out_stride, void* residual_out, int64_t res_out_stride, void* ws,
+                                     hipStream_t stream);
 hipError_t launch_lm_head_greedy(const void* x, int64_t x_stride, const int32_t* cu_rows,
                                  const void* w, int64_t w_stride, int32_t rows, int32_t vocab,
                                  int32_t k_dim, unsigned long long* keys, int32_t* ids,

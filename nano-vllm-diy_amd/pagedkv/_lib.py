@@ -60,9 +60,21 @@ SIGNATURES = {
     "pk_lm_head_greedy": (ctypes.c_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p,
         _c_void_p]),
+    "pk_linear_workspace_bytes": (_size_t, [_i32, _i32, _i32, _i32]),
+    "pk_linear": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _i64,   # x, its row stride, weight, its row stride
+        _i32, _i32, _i32, _i32,             # rows, n_out, k, epilogue
+        _c_void_p, _i64,                    # out, out_row_stride
+        _c_void_p, _size_t, _c_void_p]),    # workspace, workspace_bytes, stream
+    "pk_linear_add_rmsnorm": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _i64,   # x, its row stride, weight, its row stride
+        _i32, _i32, _i32,                   # rows, hidden, k
+        _c_void_p, _i64, _c_void_p, ctypes.c_float,  # residual, its row stride, norm weight, eps
+        _c_void_p, _i64, _c_void_p, _i64,   # out, its row stride, residual_out, its row stride
+        _c_void_p, _size_t, _c_void_p]),    # workspace, workspace_bytes, stream
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

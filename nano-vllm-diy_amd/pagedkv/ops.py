@@ -75,7 +75,8 @@ def workspace_bytes(num_seqs: int, num_heads: int, head_dim: int, max_seqlen_q: 
         num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k))
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+def _workspace(nbytes: int, device: torch.device,
+               cache: dict[int, torch.Tensor] = _workspaces) -> torch.Tensor | None:
     """Per-device scratch, grown outside graph capture and reused afterwards.
 
     Under capture a too-small cached buffer is not replaced (that would free memory a
@@ -85,12 +86,12 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
     if nbytes == 0:
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _workspaces.get(idx)
+    ws = cache.get(idx)
     if ws is not None and ws.numel() >= nbytes:
         return ws
     fresh = torch.empty(nbytes, dtype=torch.uint8, device=device)
     if not torch.cuda.is_current_stream_capturing():
-        _workspaces[idx] = fresh
+        cache[idx] = fresh
     return fresh
 
 
@@ -368,3 +369,84 @@ def lm_head_greedy(hidden_states: torch.Tensor, weight: torch.Tensor,
         weight.stride(0), rows, weight.shape[0], hidden, keys.data_ptr(), out.data_ptr(),
         _stream(hidden_states)), "pk_lm_head_greedy")
     return out
+
+
+# ----------------------------------------------------------- decode-step linear layers ---
+LINEAR_MAX_ROWS = 128
+LINEAR_STORE, LINEAR_SILU_MUL, LINEAR_ADD_RMSNORM = 0, 1, 2
+_lin_workspaces: dict[int, torch.Tensor] = {}  # device index -> cached linear-layer scratch
+
+
+def linear_workspace_bytes(rows: int, n_out: int, k: int, epilogue: int = LINEAR_STORE) -> int:
+    """Scratch bytes of one decode-step linear call (0 when it needs none)."""
+    return int(lib().pk_linear_workspace_bytes(rows, n_out, k, epilogue))
+
+
+def reserve_linear_workspace(nbytes: int, device: torch.device | str = "cuda") -> None:
+    """Grow the cached linear-layer scratch ahead of graph capture (call outside capture)."""
+    _workspace(nbytes, torch.device(device), _lin_workspaces)
+
+
+def _linear_args(x: torch.Tensor, weight: torch.Tensor, rows_per_out: int):
+    _rows2d("x", x)
+    _rows2d("weight", weight)
+    rows, k = x.shape
+    if weight.shape[1] != k or weight.shape[0] % rows_per_out:
+        raise ValueError(f"weight {tuple(weight.shape)} does not match x {tuple(x.shape)}")
+    if rows > LINEAR_MAX_ROWS:
+        raise ValueError(f"decode-step linear layers take at most {LINEAR_MAX_ROWS} rows, got {rows}")
+    return rows, k, weight.shape[0] // rows_per_out
+
+
+def _linear_call(x, weight, rows, k, n_out, epilogue, out):
+    nbytes = linear_workspace_bytes(rows, n_out, k, epilogue)
+    ws = _workspace(nbytes, x.device, _lin_workspaces)
+    check(lib().pk_linear(
+        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n_out, k, epilogue,
+        out.data_ptr(), out.stride(0), ws.data_ptr() if ws is not None else 0, nbytes,
+        _stream(x)), "pk_linear")
+    return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x, weight) of a decode step (src/layers/linear.py:74-75, :169-170): bf16
+    (rows <= 128, k) x (n_out, k)^T with fp32 accumulation, rounded to bf16."""
+    rows, k, n_out = _linear_args(x, weight, 1)
+    if out is None:
+        out = torch.empty(rows, n_out, dtype=torch.bfloat16, device=x.device)
+    return _linear_call(x, weight, rows, k, n_out, LINEAR_STORE, out)
+
+
+def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SiluAndMul(F.linear(x, weight)) for the merged gate/up weight (2 inter, k)
+    (qwen3.py:120-121): gate and up outputs are rounded to bf16, then silu(g) * u in fp32."""
+    rows, k, inter = _linear_args(x, weight, 2)
+    if out is None:
+        out = torch.empty(rows, inter, dtype=torch.bfloat16, device=x.device)
+    return _linear_call(x, weight, rows, k, inter, LINEAR_SILU_MUL, out)
+
+
+def linear_add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                       norm_weight: torch.Tensor, eps: float, out: torch.Tensor | None = None,
+                       residual_out: torch.Tensor | None = None):
+    """RMSNorm.residual_forward (layernorm.py:18-28) of h = F.linear(x, weight) and residual:
+    returns (bf16(w * s * rsqrt(mean(s^2) + eps)), bf16(s)) with s = h + residual in fp32.
+    residual_out may be residual itself (updated in place)."""
+    rows, k, hidden = _linear_args(x, weight, 1)
+    _rows2d("residual", residual)
+    if residual.shape != (rows, hidden):
+        raise ValueError(f"residual must be ({rows}, {hidden})")
+    if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != hidden or not norm_weight.is_contiguous():
+        raise ValueError("norm_weight must be a contiguous (hidden,) bf16 tensor")
+    if out is None:
+        out = torch.empty(rows, hidden, dtype=torch.bfloat16, device=x.device)
+    if residual_out is None:
+        residual_out = torch.empty_like(residual)
+    nbytes = linear_workspace_bytes(rows, hidden, k, LINEAR_ADD_RMSNORM)
+    ws = _workspace(nbytes, x.device, _lin_workspaces)
+    check(lib().pk_linear_add_rmsnorm(
+        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, hidden, k,
+        residual.data_ptr(), residual.stride(0), norm_weight.data_ptr(), float(eps),
+        out.data_ptr(), out.stride(0), residual_out.data_ptr(), residual_out.stride(0),
+        ws.data_ptr() if ws is not None else 0, nbytes, _stream(x)), "pk_linear_add_rmsnorm")
+    return out, residual_out

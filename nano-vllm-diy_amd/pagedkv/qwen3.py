@@ -75,20 +75,39 @@ class Qwen3Model:
         self.cos_sin = ops.rope_cos_sin(max_position, cfg.head_dim, cfg.rope_theta, dev)
         self.scale = cfg.head_dim ** -0.5
 
+    def linear_workspace_bytes(self, rows: int) -> int:
+        """Scratch the decode-step linear layers need for a batch of `rows` tokens."""
+        if rows > ops.LINEAR_MAX_ROWS:
+            return 0
+        cfg = self.cfg
+        H, qd, inter = cfg.hidden_size, cfg.num_attention_heads * cfg.head_dim, cfg.intermediate_size
+        qkv_out = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+        return max(ops.linear_workspace_bytes(rows, qkv_out, H, ops.LINEAR_STORE),
+                   ops.linear_workspace_bytes(rows, H, qd, ops.LINEAR_ADD_RMSNORM),
+                   ops.linear_workspace_bytes(rows, inter, H, ops.LINEAR_SILU_MUL),
+                   ops.linear_workspace_bytes(rows, H, inter, ops.LINEAR_ADD_RMSNORM))
+
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, ctx: Context) -> torch.Tensor:
+        """Steps of at most 128 tokens (decode batches) run every projection on the library's
+        decode-step linear kernels, each fused with the op after it: qkv_proj; o_proj + the
+        post-attention RMSNorm; gate_up_proj + SiluAndMul; down_proj + the next layer's input
+        RMSNorm (the final norm after the last layer). Larger steps use F.linear (a library
+        GEMM) and the separate norm / activation kernels. Rounding points are the same."""
         cfg, W = self.cfg, self.w
         Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         eps = cfg.rms_norm_eps
         flat = ctx.block_tables is None
+        small = input_ids.shape[0] <= ops.LINEAR_MAX_ROWS
         h = F.embedding(input_ids, W.embed)
         residual = None
+        nl = len(W.layers)
         for li, L in enumerate(W.layers):
             if residual is None:
                 x = ops.add_rmsnorm(h, L["input_norm"], eps)
                 residual = h
-            else:
+            elif not small:
                 x, residual = ops.add_rmsnorm(h, L["input_norm"], eps, residual=residual)
-            qkv = F.linear(x, L["qkv"])
+            qkv = ops.linear(x, L["qkv"]) if small else F.linear(x, L["qkv"])
             kc, vc = self.k_caches[li], self.v_caches[li]
             q, k = ops.qk_norm_rope_store(qkv, positions, self.cos_sin, Hq, Hkv, D, L["q_norm"],
                                           L["k_norm"], eps, kc, vc, ctx.slot_mapping, return_k=flat)
@@ -100,10 +119,18 @@ class Qwen3Model:
                 o = ops.varlen_attention(q, kc, vc, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
                                          ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True,
                                          ctx.block_tables)
-            h = F.linear(o.view(-1, Hq * D), L["o"])
-            x, residual = ops.add_rmsnorm(h, L["post_norm"], eps, residual=residual)
-            h = F.linear(ops.silu_and_mul(F.linear(x, L["gate_up"])), L["down"])
-        x, _ = ops.add_rmsnorm(h, W.final_norm, eps, residual=residual)
+            if small:
+                x, residual = ops.linear_add_rmsnorm(o.view(-1, Hq * D), L["o"], residual,
+                                                     L["post_norm"], eps, residual_out=residual)
+                nxt = W.layers[li + 1]["input_norm"] if li + 1 < nl else W.final_norm
+                x, residual = ops.linear_add_rmsnorm(ops.linear_silu_mul(x, L["gate_up"]), L["down"],
+                                                     residual, nxt, eps, residual_out=residual)
+            else:
+                h = F.linear(o.view(-1, Hq * D), L["o"])
+                x, residual = ops.add_rmsnorm(h, L["post_norm"], eps, residual=residual)
+                h = F.linear(ops.silu_and_mul(F.linear(x, L["gate_up"])), L["down"])
+        if not small:
+            x, _ = ops.add_rmsnorm(h, W.final_norm, eps, residual=residual)
         return x
 
     def greedy(self, hidden: torch.Tensor, ctx: Context, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -106,6 +106,7 @@ class ModelRunner:
         # buffers the kernels reuse inside the graphs, sized for the largest batch up front
         ops.reserve_workspace(max_bs, self.cfg.num_attention_heads, self.cfg.head_dim, 1,
                               self.max_seq_len, self.dev)
+        ops.reserve_linear_workspace(self.model.linear_workspace_bytes(max_bs), self.dev)
         ops.lm_head_greedy(torch.zeros(max_bs, self.cfg.hidden_size, dtype=torch.bfloat16,
                                        device=self.dev), self.weights.embed)
         pool = None

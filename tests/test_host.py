@@ -181,3 +181,52 @@ def test_producer_argument_checks_fail_before_launch():
     assert b"aligned" in lib.pk_last_error()
     assert _prod(lib, max_position=0) == _lib.PK_ERR_INVALID_ARG
     assert _prod(lib, eps=-1.0) == _lib.PK_ERR_INVALID_ARG
+
+
+# ---------------------------------------------------------------- decode-step linear ---
+_FAKE = 1 << 32  # 16-byte aligned fake device addresses: these calls fail before any HIP call
+
+
+def _linear(lib, x=_FAKE, xs=1024, w=2 * _FAKE, ws_=1024, rows=8, n_out=4096, k=1024, epi=0,
+            out=3 * _FAKE, os_=4096, work=4 * _FAKE, work_bytes=1 << 30):
+    return lib.pk_linear(x, xs, w, ws_, rows, n_out, k, epi, out, os_, work, work_bytes, None)
+
+
+def test_linear_argument_checks():
+    lib = _lib.lib()
+    assert _linear(lib, rows=129) == _lib.PK_ERR_UNSUPPORTED            # decode batches only
+    assert _linear(lib, k=1000) == _lib.PK_ERR_UNSUPPORTED              # k % 256
+    assert _linear(lib, n_out=100, os_=104) == _lib.PK_ERR_UNSUPPORTED  # n_out % 32
+    assert _linear(lib, epi=2) == _lib.PK_ERR_INVALID_ARG               # norm has its own entry
+    assert _linear(lib, xs=1000) == _lib.PK_ERR_INVALID_ARG             # stride below k
+    assert _linear(lib, x=_FAKE + 8) == _lib.PK_ERR_INVALID_ARG         # misaligned
+    assert _linear(lib, w=None) == _lib.PK_ERR_INVALID_ARG
+    # out overlapping x (same buffer) is refused; adjacent buffers are fine up to the launch
+    assert _linear(lib, out=_FAKE + 2 * 1024 * 7) == _lib.PK_ERR_INVALID_ARG
+    need = lib.pk_linear_workspace_bytes(8, 4096, 1024, 0)
+    assert need > 0
+    assert _linear(lib, work_bytes=need - 1) == _lib.PK_ERR_WORKSPACE
+    assert _linear(lib, rows=0) == _lib.PK_OK
+    rc = lib.pk_linear_add_rmsnorm(_FAKE, 2048, 2 * _FAKE, 2048, 8, 1024, 2048, None, 1024,
+                                   5 * _FAKE, 1e-6, 3 * _FAKE, 1024, 6 * _FAKE, 1024,
+                                   4 * _FAKE, 1 << 30, None)
+    assert rc == _lib.PK_ERR_INVALID_ARG                               # residual required
+    rc = lib.pk_linear_add_rmsnorm(_FAKE, 8192, 2 * _FAKE, 8192, 8, 8192, 8192, 7 * _FAKE, 8192,
+                                   5 * _FAKE, 1e-6, 3 * _FAKE, 8192, 6 * _FAKE, 8192,
+                                   4 * _FAKE, 1 << 30, None)
+    assert rc == _lib.PK_ERR_UNSUPPORTED                               # hidden above 4096
+
+
+def test_linear_workspace_sizes():
+    lib = _lib.lib()
+    f = lib.pk_linear_workspace_bytes
+    assert f(0, 4096, 1024, 0) == 0 and f(129, 4096, 1024, 0) == 0
+    for n_out, k, epi in [(4096, 1024, 0), (3072, 1024, 1), (1024, 2048, 2), (1024, 3072, 2)]:
+        one = f(1, n_out, k, epi)
+        # fp32 partial sums of every row: a whole number of row-sized slabs, linear in rows
+        slab = n_out * 4 * (2 if epi == 1 else 1)
+        assert one > 0 and one % slab == 0 and (k // 256) % (one // slab) == 0
+        assert f(128, n_out, k, epi) == 128 * one
+    # enough tiles without splitting K: no scratch, except the norm epilogue (whole rows)
+    assert f(64, 8192, 1024, 0) == 0
+    assert f(64, 1024, 256, 2) == 64 * 1024 * 4
