@@ -12,12 +12,16 @@
 //
 // At these row counts the work is reading the weight once: 4-12 MB per projection for
 // Qwen3-0.6B against at most 0.8 MB of x. The weight is cut into 32-row tiles (one MFMA
-// tile; 32 gate + 32 up rows for SiLU * mul) and, when there are fewer tiles than CUs, its
-// K range into KS equal splits, so enough work-groups stream it at once. A work-group's
-// four wavefronts take interleaved 64-wide K blocks of its range and add their
-// accumulators through LDS. With KS = 1 the epilogue runs in the work-group; otherwise
-// fp32 partial sums go to the workspace and a second kernel adds them and applies it
-// (the residual-add + RMSNorm epilogue needs whole rows and always takes that path).
+// tile; 32 gate + 32 up rows for SiLU * mul) and the token rows into 32-row tiles; a
+// work-group owns one weight tile, MT row tiles and a K range. Row groups of one weight
+// tile are consecutive multiples of the tile count apart in the grid, so they run on one
+// XCD and read the weight tile from HBM once, through that XCD's L2. The K range is split
+// (KS > 1) only when the (weight tile x row group) grid is too small to keep the CUs
+// streaming. A work-group's four wavefronts take interleaved 64-wide K blocks of its range,
+// issue the loads of up to four blocks before the first MFMA, and add their accumulators
+// through LDS. With KS = 1 the epilogue runs in the work-group; otherwise fp32 partial sums
+// go to the workspace and a second kernel adds them and applies it (the residual-add +
+// RMSNorm epilogue needs whole rows and always takes that path).
 //
 // MFMA: v_mfma_f32_32x32x16_bf16 with D = W_tile (32 x 16) . x^T (16 x 32 rows). In K
 // block kb, step q, lane (r, h) supplies weight row r and x row c = r at K positions
@@ -32,12 +36,25 @@ namespace {
 constexpr int kLinThreads = 256;   // four wavefronts
 constexpr int kLinTile = 32;       // weight rows (output columns) per tile
 constexpr int kLinKBlock = 64;     // K elements per wavefront block (4 MFMA steps)
+constexpr int kLinChunk = 4 * kLinKBlock;  // K elements per LDS stage (one block per wavefront)
 #ifndef PK_LINEAR_TARGET_GROUPS
 #define PK_LINEAR_TARGET_GROUPS 256
 #endif
-constexpr int kLinTargetGroups = PK_LINEAR_TARGET_GROUPS;  // work-groups a launch aims for
+#ifndef PK_LINEAR_MIN_GROUPS
+#define PK_LINEAR_MIN_GROUPS 64
+#endif
+#ifndef PK_LINEAR_MT2_ROWS
+#define PK_LINEAR_MT2_ROWS 64
+#endif
+constexpr int kLinTargetGroups = PK_LINEAR_TARGET_GROUPS;  // work-groups a split launch aims for
+constexpr int kLinMinGroups = PK_LINEAR_MIN_GROUPS;        // smallest grid left unsplit
+constexpr int kLinMaxChunks = 4;                           // longest unsplit K walk (chunks)
+constexpr int kLinMt2Rows = PK_LINEAR_MT2_ROWS;            // more rows: two row tiles per group
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+// 16-byte register value for the staged loads (a native vector: HIP's uint4 struct is
+// copied through private memory by the staging loops)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float gb = bf16_lo(pack_bf16x2(g, 0.f));  // g and u rounded to bf16 (the GEMM output)
@@ -61,25 +78,68 @@ struct LinArgs {
   float* part;       // [ks][rows][np * n_out] fp32 partial sums
 };
 
-// NP = weight tiles per work-group (2: gate rows n0.., up rows n_out + n0..); MT = 32-row x tiles.
-template <int NP, int MT, int EPI>
+// Waits for this wavefront's LDS operations, then for every wavefront of the work-group.
+// s_waitcnt lgkmcnt(0) on its own: __syncthreads() would also wait for vmcnt(0), i.e. for
+// the global loads of later K chunks that are still in flight.
+__device__ __forceinline__ void lin_lds_barrier() {
+  __builtin_amdgcn_s_waitcnt((15 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0) only
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// NP = weight tiles per work-group (2: gate rows n0.., up rows n_out + n0..); MT = 32-row x
+// tiles per work-group; NB = 256-wide K chunks whose global loads are issued together.
+//
+// Loads: a 32-row x 256-column operand tile (16 KB) is read by the 256 threads as four
+// instructions of 8 rows x 512 contiguous bytes (thread t: row 8 i + t / 32, 16-byte
+// column t % 32), so every 4-lane quad reads 64 bytes of one row. (Loading the MFMA layout
+// straight from memory puts 32 different rows in one instruction and 4 in every quad,
+// which costs four L1 tag lookups per quad.) The tile goes to LDS with 16-byte column c of
+// row r at r * 512 + ((c ^ r) & 31) * 16, so the stores and the MFMA operand reads
+// (16 lanes = 16 rows of one column) are free of bank conflicts. Two LDS stages: chunk c
+// is stored in stage c & 1 while the other stage may still be read for chunk c - 1.
+// Wavefront w multiplies the 64 columns [64 w, 64 w + 64) of every chunk.
+template <int NP, int MT, int NB, int EPI>
 __global__ __launch_bounds__(kLinThreads) void linear_kernel(const LinArgs a) {
-  __shared__ float4 red[4][NP][4][kWave];  // one x-row tile of every wavefront's accumulators
+  constexpr int kOps = NP + MT;               // operand tiles per chunk
+  constexpr int kTileBytes = 32 * kLinChunk * 2;
+  constexpr int kStage = kOps * kTileBytes;
+  constexpr int kRedBytes = 4 * NP * 4 * kWave * 16;
+  constexpr int kSmem = 2 * kStage > kRedBytes ? 2 * kStage : kRedBytes;
+  __shared__ __attribute__((aligned(16))) char smem[kSmem];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int r = lane & 31, h = lane >> 5;
-  const int ntile = blockIdx.x % (a.n_out / kLinTile);
-  const int split = blockIdx.x / (a.n_out / kLinTile);
-  const int n0 = ntile * kLinTile;
+  const int ntiles = a.n_out / kLinTile;
+  const int per_group = ntiles * a.ks;  // work-groups of one row group
+  const int mgroup = blockIdx.x / per_group;
+  const int rem = blockIdx.x - mgroup * per_group;
+  const int split = rem / ntiles;
+  const int n0 = (rem - split * ntiles) * kLinTile;
+  const int row0 = mgroup * MT * 32;
   const int kc = a.k / a.ks;
   const int kbeg = split * kc;
 
-  const uint16_t* wrow[NP];
+  // loader: thread row lr (+ 8 i), 16-byte column lc
+  const int lr = threadIdx.x >> 5, lc = threadIdx.x & 31;
+  const uint16_t* src[kOps][4];
 #pragma unroll
-  for (int p = 0; p < NP; ++p) wrow[p] = a.w + (int64_t)(p * a.n_out + n0 + r) * a.w_stride + 32 * h;
-  const uint16_t* xrow[MT];
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-  for (int t = 0; t < MT; ++t) xrow[t] = a.x + (int64_t)min(32 * t + r, a.rows - 1) * a.x_stride + 32 * h;
+    for (int p = 0; p < NP; ++p)
+      src[p][i] = a.w + (int64_t)(p * a.n_out + n0 + 8 * i + lr) * a.w_stride + kbeg + 8 * lc;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      src[NP + t][i] =
+          a.x + (int64_t)min(row0 + 32 * t + 8 * i + lr, a.rows - 1) * a.x_stride + kbeg + 8 * lc;
+  }
+  int wofs[4], rofs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * i + lr;
+    wofs[i] = row * (2 * kLinChunk) + ((lc ^ row) & 31) * 16;
+    const int cc = 8 * wave + 4 * h + i;  // MFMA step i reads 16-byte column cc of row r
+    rofs[i] = r * (2 * kLinChunk) + ((cc ^ r) & 31) * 16;
+  }
 
   f32x16 acc[NP][MT];
 #pragma unroll
@@ -89,45 +149,44 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(const LinArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[p][t][i] = 0.f;
 
-  // blocks kbeg + 64 (wave + 4 j): the next block's weight is in flight during this one
-  const int nblk = kc / kLinKBlock;
-  uint4 wa[NP][4], wn[NP][4];
-  int b = wave;
-  if (b < nblk) {
+  const int nch = kc / kLinChunk;
+  for (int j0 = 0; j0 < nch; j0 += NB) {
+    u32x4_t st[NB][kOps][4];
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) wa[p][q] = *reinterpret_cast<const uint4*>(wrow[p] + kbeg + b * kLinKBlock + 8 * q);
-  }
-  for (; b < nblk; b += 4) {
-    const int kb = kbeg + b * kLinKBlock;
-    const bool more = b + 4 < nblk;
-    if (more) {
+      for (int o = 0; o < kOps; ++o)
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+        for (int i = 0; i < 4; ++i)
+          st[j][o][i] = *reinterpret_cast<const u32x4_t*>(src[o][i] + (j0 + j) * kLinChunk);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wn[p][q] = *reinterpret_cast<const uint4*>(wrow[p] + kb + 4 * kLinKBlock + 8 * q);
-    }
-    uint4 xb[MT][4];
+    for (int j = 0; j < NB; ++j) {
+      char* stage = smem + ((j0 + j) & 1) * kStage;
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+      for (int o = 0; o < kOps; ++o)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xb[t][q] = *reinterpret_cast<const uint4*>(xrow[t] + kb + 8 * q);
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(stage + o * kTileBytes + wofs[i]) = st[j][o][i];
+      lin_lds_barrier();
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < 4; ++q) {
+        u32x4_t xv[MT];
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
+        for (int t = 0; t < MT; ++t) xv[t] = *reinterpret_cast<const u32x4_t*>(stage + (NP + t) * kTileBytes + rofs[q]);
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-          acc[p][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, wa[p][q]),
-                                                              __builtin_bit_cast(bf16x8_t, xb[t][q]), acc[p][t], 0, 0, 0);
-    if (more) {
+        for (int p = 0; p < NP; ++p) {
+          const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(stage + p * kTileBytes + rofs[q]);
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) wa[p][q] = wn[p][q];
+          for (int t = 0; t < MT; ++t)
+            acc[p][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, wv),
+                                                                __builtin_bit_cast(bf16x8_t, xv[t]),
+                                                                acc[p][t], 0, 0, 0);
+        }
+      }
     }
   }
+  __syncthreads();  // every wavefront is done with the stages before they hold the sums
+  auto red = reinterpret_cast<float4 (*)[NP][4][kWave]>(smem);
 
   // Add the four wavefronts' accumulators one x-row tile at a time. Thread (c, q) then owns
   // x row 32 t + c and the 4 output columns n0 + 4 q .. + 3: D elements 4 (q >> 1) .. + 3 of
@@ -144,7 +203,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(const LinArgs a) {
         red[wave][p][j][lane] = make_float4(acc[p][t][4 * j], acc[p][t][4 * j + 1], acc[p][t][4 * j + 2],
                                             acc[p][t][4 * j + 3]);
     __syncthreads();
-    const int m = 32 * t + c;
+    const int m = row0 + 32 * t + c;
     float4 v[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -270,36 +329,72 @@ __global__ __launch_bounds__(kLinNormThreads) void linear_add_rmsnorm_kernel(
   }
 }
 
-// K splits: the smallest divisor KS of K / 256 whose tiles x KS reach kLinTargetGroups
-// work-groups (every wavefront gets at least one 64-wide block per split), else K / 256.
-int choose_splits(int tiles, int k) {
-  const int blocks = k / (4 * kLinKBlock);
-  for (int s = 1; s < blocks; ++s)
-    if (blocks % s == 0 && (int64_t)tiles * s >= kLinTargetGroups) return s;
-  return blocks;
+// Launch shape: MT row tiles per work-group, row groups, K splits, blocks per load batch.
+struct LinCfg {
+  int mt, mgroups, ks, nb;
+};
+
+// K is left unsplit when the grid of (weight tile x 32-row tile) work-groups has at least
+// kLinMinGroups entries and a work-group then walks at most kLinMaxChunks 256-wide
+// chunks; otherwise KS is the smallest divisor of K / 256 whose grid reaches
+// kLinTargetGroups (K / 256 at most). KS does not depend on the epilogue, so every
+// epilogue sums the same products in the same order and the fused entry points equal
+// linear + the standalone epilogue kernels bit for bit. The merged gate / up weight
+// (np = 2) takes two row tiles per work-group above kLinMt2Rows rows, which keeps its
+// grid within one work-group per CU (its stages take 128 KB of LDS); row tiles do not
+// change any sum. Wavefronts batch the loads of up to four chunks.
+LinCfg choose_config(int rows, int tiles, int k, int np) {
+  LinCfg c{};
+  const int64_t base = (int64_t)tiles * ((rows + 31) / 32);
+  const int blocks = k / kLinChunk;
+  c.ks = blocks;
+  if (base >= kLinMinGroups && blocks <= kLinMaxChunks) {
+    c.ks = 1;
+  } else {
+    for (int s = 1; s < blocks; ++s)
+      if (blocks % s == 0 && base * s >= kLinTargetGroups) {
+        c.ks = s;
+        break;
+      }
+  }
+  c.mt = np == 2 && rows > kLinMt2Rows ? 2 : 1;
+  c.mgroups = (rows + 32 * c.mt - 1) / (32 * c.mt);
+  const int chunks = blocks / c.ks;  // 256-wide K chunks per work-group
+  c.nb = chunks % 4 == 0 ? 4 : chunks % 2 == 0 ? 2 : 1;
+  return c;
 }
 
-template <int NP, int EPI>
-hipError_t launch_main(const LinArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.n_out / kLinTile) * a.ks));
-  const int mt = (a.rows + 31) / 32;
-  switch (mt) {
-    case 1: hipLaunchKernelGGL((linear_kernel<NP, 1, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((linear_kernel<NP, 2, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
-    case 3: hipLaunchKernelGGL((linear_kernel<NP, 3, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((linear_kernel<NP, 4, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
+template <int NP, int MT, int EPI>
+hipError_t launch_nb(const LinArgs& a, const LinCfg& c, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.n_out / kLinTile) * a.ks * c.mgroups));
+  // at most 128 staging registers per lane: 16 per operand tile and chunk
+  const int nb = (NP + MT) * 16 * c.nb > 128 ? c.nb / 2 : c.nb;
+  switch (nb) {
+    case 1: hipLaunchKernelGGL((linear_kernel<NP, MT, 1, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((linear_kernel<NP, MT, 2, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((linear_kernel<NP, MT, 4, EPI>), grid, dim3(kLinThreads), 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int NP, int EPI>
+hipError_t launch_main(const LinArgs& a, const LinCfg& c, hipStream_t stream) {
+  switch (c.mt) {
+    case 1: return launch_nb<NP, 1, EPI>(a, c, stream);
+    case 2: return launch_nb<NP, 2, EPI>(a, c, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
 
 size_t linear_workspace_bytes(int32_t rows, int32_t n_out, int32_t k, int32_t epilogue) {
   if (rows <= 0 || n_out <= 0 || k <= 0) return 0;
-  const int ks = choose_splits(n_out / kLinTile, k);
-  if (ks == 1 && epilogue != kLinearAddRmsNorm) return 0;
-  return (size_t)ks * rows * (epilogue == kLinearSiluMul ? 2 : 1) * n_out * sizeof(float);
+  const bool partial = epilogue == kLinearAddRmsNorm;
+  const LinCfg c = choose_config(rows, n_out / kLinTile, k, epilogue == kLinearSiluMul ? 2 : 1);
+  if (c.ks == 1 && !partial) return 0;
+  return (size_t)c.ks * rows * (epilogue == kLinearSiluMul ? 2 : 1) * n_out * sizeof(float);
 }
 
 hipError_t launch_linear(const void* x, int64_t x_stride, const void* w, int64_t w_stride, int32_t rows,
@@ -313,13 +408,14 @@ hipError_t launch_linear(const void* x, int64_t x_stride, const void* w, int64_t
   a.rows = rows;
   a.n_out = n_out;
   a.k = k;
-  a.ks = choose_splits(n_out / kLinTile, k);
+  const LinCfg c = choose_config(rows, n_out / kLinTile, k, epilogue == kLinearSiluMul ? 2 : 1);
+  a.ks = c.ks;
   a.y = static_cast<uint16_t*>(y);
   a.y_stride = y_stride;
   a.part = static_cast<float*>(ws);
   const bool pair = epilogue == kLinearSiluMul;
-  if (a.ks == 1) return pair ? launch_main<2, kEpiSiluMul>(a, stream) : launch_main<1, kEpiStore>(a, stream);
-  hipError_t err = pair ? launch_main<2, kEpiPartial>(a, stream) : launch_main<1, kEpiPartial>(a, stream);
+  if (a.ks == 1) return pair ? launch_main<2, kEpiSiluMul>(a, c, stream) : launch_main<1, kEpiStore>(a, c, stream);
+  hipError_t err = pair ? launch_main<2, kEpiPartial>(a, c, stream) : launch_main<1, kEpiPartial>(a, c, stream);
   if (err != hipSuccess) return err;
   const int64_t total = (int64_t)rows * (n_out / 8);
   const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1024);
@@ -343,9 +439,10 @@ hipError_t launch_linear_add_rmsnorm(const void* x, int64_t x_stride, const void
   a.rows = rows;
   a.n_out = n_out;
   a.k = k;
-  a.ks = choose_splits(n_out / kLinTile, k);
+  const LinCfg c = choose_config(rows, n_out / kLinTile, k, 1);
+  a.ks = c.ks;
   a.part = static_cast<float*>(ws);
-  hipError_t err = launch_main<1, kEpiPartial>(a, stream);
+  hipError_t err = launch_main<1, kEpiPartial>(a, c, stream);
   if (err != hipSuccess) return err;
   const int vecs = (n_out / 8 + kLinNormThreads - 1) / kLinNormThreads;
   auto* rp = static_cast<const uint16_t*>(residual);

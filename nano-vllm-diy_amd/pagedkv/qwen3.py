@@ -75,17 +75,19 @@ class Qwen3Model:
         self.cos_sin = ops.rope_cos_sin(max_position, cfg.head_dim, cfg.rope_theta, dev)
         self.scale = cfg.head_dim ** -0.5
 
-    def linear_workspace_bytes(self, rows: int) -> int:
-        """Scratch the decode-step linear layers need for a batch of `rows` tokens."""
-        if rows > ops.LINEAR_MAX_ROWS:
-            return 0
+    def linear_workspace_bytes(self, max_rows: int) -> int:
+        """Scratch the decode-step linear layers need for any batch of up to `max_rows`
+        tokens (the launch shape, and so the scratch, depends on the row count)."""
         cfg = self.cfg
         H, qd, inter = cfg.hidden_size, cfg.num_attention_heads * cfg.head_dim, cfg.intermediate_size
         qkv_out = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
-        return max(ops.linear_workspace_bytes(rows, qkv_out, H, ops.LINEAR_STORE),
-                   ops.linear_workspace_bytes(rows, H, qd, ops.LINEAR_ADD_RMSNORM),
-                   ops.linear_workspace_bytes(rows, inter, H, ops.LINEAR_SILU_MUL),
-                   ops.linear_workspace_bytes(rows, H, inter, ops.LINEAR_ADD_RMSNORM))
+        need = 0
+        for rows in range(1, min(max_rows, ops.LINEAR_MAX_ROWS) + 1):
+            need = max(need, ops.linear_workspace_bytes(rows, qkv_out, H, ops.LINEAR_STORE),
+                       ops.linear_workspace_bytes(rows, H, qd, ops.LINEAR_ADD_RMSNORM),
+                       ops.linear_workspace_bytes(rows, inter, H, ops.LINEAR_SILU_MUL),
+                       ops.linear_workspace_bytes(rows, H, inter, ops.LINEAR_ADD_RMSNORM))
+        return need
 
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, ctx: Context) -> torch.Tensor:
         """Steps of at most 128 tokens (decode batches) run every projection on the library's

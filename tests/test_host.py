@@ -203,9 +203,10 @@ def test_linear_argument_checks():
     assert _linear(lib, w=None) == _lib.PK_ERR_INVALID_ARG
     # out overlapping x (same buffer) is refused; adjacent buffers are fine up to the launch
     assert _linear(lib, out=_FAKE + 2 * 1024 * 7) == _lib.PK_ERR_INVALID_ARG
-    need = lib.pk_linear_workspace_bytes(8, 4096, 1024, 0)
+    need = lib.pk_linear_workspace_bytes(8, 1024, 2048, 0)  # few weight tiles: K is split
     assert need > 0
-    assert _linear(lib, work_bytes=need - 1) == _lib.PK_ERR_WORKSPACE
+    assert _linear(lib, n_out=1024, k=2048, xs=2048, ws_=2048, os_=1024, work_bytes=need - 1) == _lib.PK_ERR_WORKSPACE
+    assert _linear(lib, n_out=1024, k=2048, xs=2048, ws_=2048, os_=1024, work=None) == _lib.PK_ERR_WORKSPACE
     assert _linear(lib, rows=0) == _lib.PK_OK
     rc = lib.pk_linear_add_rmsnorm(_FAKE, 2048, 2 * _FAKE, 2048, 8, 1024, 2048, None, 1024,
                                    5 * _FAKE, 1e-6, 3 * _FAKE, 1024, 6 * _FAKE, 1024,
@@ -222,11 +223,16 @@ def test_linear_workspace_sizes():
     f = lib.pk_linear_workspace_bytes
     assert f(0, 4096, 1024, 0) == 0 and f(129, 4096, 1024, 0) == 0
     for n_out, k, epi in [(4096, 1024, 0), (3072, 1024, 1), (1024, 2048, 2), (1024, 3072, 2)]:
-        one = f(1, n_out, k, epi)
-        # fp32 partial sums of every row: a whole number of row-sized slabs, linear in rows
-        slab = n_out * 4 * (2 if epi == 1 else 1)
-        assert one > 0 and one % slab == 0 and (k // 256) % (one // slab) == 0
-        assert f(128, n_out, k, epi) == 128 * one
-    # enough tiles without splitting K: no scratch, except the norm epilogue (whole rows)
+        slab = n_out * 4 * (2 if epi == 1 else 1)  # fp32 partial sums of one row
+        for rows in (1, 17, 32, 33, 64, 100, 128):
+            need = f(rows, n_out, k, epi)
+            if need == 0:
+                assert epi != 2                   # the norm epilogue always takes the partial path
+                continue
+            # K splits x rows whole slabs, the split count dividing k / 256
+            assert need % (rows * slab) == 0 and (k // 256) % (need // (rows * slab)) == 0
+    # enough (weight tile x row group) work-groups without splitting K: no scratch, except
+    # for the norm epilogue (whole rows), which keeps one slab per row
     assert f(64, 8192, 1024, 0) == 0
+    assert f(128, 4096, 1024, 0) == 0
     assert f(64, 1024, 256, 2) == 64 * 1024 * 4
