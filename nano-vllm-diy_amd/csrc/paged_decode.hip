@@ -37,6 +37,12 @@ namespace {
 #ifndef PK_DECODE_SPLIT_MAX
 #define PK_DECODE_SPLIT_MAX 512 // keys per work unit (split) when the batch is large
 #endif
+#ifndef PK_DECODE_MIN_GROUPS
+#define PK_DECODE_MIN_GROUPS 2048  // work-groups a batch's grid aims for before splits stop shrinking
+#endif
+#ifndef PK_DECODE_MIN_SPLIT
+#define PK_DECODE_MIN_SPLIT 64     // shortest split (keys) the sizing goes down to
+#endif
 #ifndef PK_DECODE_NT_FROM
 // Keys at positions >= PK_DECODE_NT_FROM are read with non-temporal (streaming) loads,
 // earlier ones with normal loads. Prefix caching can only share a sequence's leading
@@ -373,7 +379,8 @@ int decode_split_tokens(int num_seqs, int max_seqlen_k) {
   // the combine pass's weight table (kCombineMaxSplits per sequence) would overflow.
   const auto splits = [&](int split) { return (int64_t)(max_seqlen_k + split - 1) / split; };
   int split = PK_DECODE_SPLIT_MAX;
-  while (split > 64 && (int64_t)num_seqs * splits(split) < 2048 && splits(split / 2) <= kCombineMaxSplits)
+  while (split > PK_DECODE_MIN_SPLIT && (int64_t)num_seqs * splits(split) < PK_DECODE_MIN_GROUPS &&
+         splits(split / 2) <= kCombineMaxSplits)
     split /= 2;
   while (splits(split) > kCombineMaxSplits) split *= 2;
   return split;
