@@ -94,9 +94,19 @@ __device__ __forceinline__ void lds_barrier() {
 // LDS tiles are stored unpadded, one 256-byte row per key, with the row's sixteen 16-byte
 // chunks XOR-swizzled so that the MFMA operand reads hit distinct banks:
 //   K: chunk c of row r lives in slot c ^ (r & 15)      (32 consecutive rows read chunk c)
-//   V: chunk c of row r lives in slot c ^ ((2 r) & 15)  (4 consecutive rows x 2 chunks read)
+//   V: chunk c of row r lives in slot c ^ ((2 r) & 15) ^ 8 (c & 2)
+// A V transpose read serves 32 lanes per cycle: two 16-lane groups, each reading 4
+// consecutive rows x 2 chunks, the second group the next two chunks. The XOR with 2 r
+// spreads a group over 8 slots; the extra 8 (c & 2) puts the second group's chunks in the
+// other 8 slots, so the 32 lanes hit all 64 banks once.
 __device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
-__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((2 * r) & 15); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((2 * r) & 15) ^ ((c & 2) << 2); }
+// Inverse of v_slot: the chunk stored in slot s of row r (bit 1 of the chunk survives the
+// first XOR, so it names the second one).
+__device__ __forceinline__ int v_chunk(int r, int s) {
+  const int y = s ^ ((2 * r) & 15);
+  return y ^ ((y & 2) << 2);
+}
 
 // Keys [t0, t0 + 64) of kv head g move global -> registers -> LDS: wavefront w owns tile
 // rows kRowsPerWave w .. kRowsPerWave (w + 1) - 1, four rows (1 KiB) per 16-byte load
@@ -125,7 +135,7 @@ __device__ __forceinline__ LoadLanes load_lanes(const AttnArgs& a, int wave, int
     const int r = kRowsPerWave * wave + 4 * i + (lane >> 4);  // tile row this lane fills
     const int rs = min(r, last);                              // source row (clamped on the last tile)
     l.k[i] = rs * (int)a.k_row_stride + (slot ^ (r & 15)) * 8;
-    l.v[i] = rs * (int)a.v_row_stride + (slot ^ ((2 * r) & 15)) * 8;
+    l.v[i] = rs * (int)a.v_row_stride + v_chunk(r, slot) * 8;
   }
   return l;
 }
