@@ -373,6 +373,36 @@ def producer_call(dev, n: int, seed: int = 6):
     return fn, n * per_token
 
 
+def linear_calls(dev, rows: int, seed: int = 7):
+    """The four decode-step projections of one Qwen3-0.6B decoder layer on `rows` tokens,
+    each with its fused epilogue: qkv (store), o + residual RMSNorm, gate/up + SiLU * mul,
+    down + residual RMSNorm. Algorithmic bytes per call: the weight (n_out x k bf16), x,
+    the outputs and, for the norm epilogue, the residual read and written."""
+    import torch
+
+    import pagedkv
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    H, Q, I, QKV = 1024, 2048, 3072, 4096
+    rnd = lambda *shape, s=1.0: (torch.randn(*shape, generator=g, device=dev) * s).to(torch.bfloat16)
+    x_h, x_q, x_i = rnd(rows, H), rnd(rows, Q), rnd(rows, I)
+    res, nw = rnd(rows, H), torch.ones(H, dtype=torch.bfloat16, device=dev)
+    w_qkv, w_o, w_gu, w_d = rnd(QKV, H, s=0.02), rnd(H, Q, s=0.02), rnd(2 * I, H, s=0.02), rnd(H, I, s=0.02)
+    y_qkv = torch.empty(rows, QKV, dtype=torch.bfloat16, device=dev)
+    y_i = torch.empty(rows, I, dtype=torch.bfloat16, device=dev)
+    y_h, r_h = torch.empty(rows, H, dtype=torch.bfloat16, device=dev), torch.empty(rows, H, dtype=torch.bfloat16,
+                                                                                   device=dev)
+    b = 2
+    return [
+        ("qkv", lambda: pagedkv.linear(x_h, w_qkv, out=y_qkv), b * (QKV * H + rows * (H + QKV))),
+        ("o_norm", lambda: pagedkv.linear_add_rmsnorm(x_q, w_o, res, nw, 1e-6, out=y_h, residual_out=r_h),
+         b * (H * Q + rows * (Q + 4 * H) + H)),
+        ("gate_up_silu", lambda: pagedkv.linear_silu_mul(x_h, w_gu, out=y_i), b * (2 * I * H + rows * (H + I))),
+        ("down_norm", lambda: pagedkv.linear_add_rmsnorm(x_i, w_d, res, nw, 1e-6, out=y_h, residual_out=r_h),
+         b * (H * I + rows * (I + 4 * H) + H)),
+    ]
+
+
 def extra_configs(dev, w2):
     """Per-kernel measurements of the other configurations (events, mean of 20 launches)."""
     import torch
@@ -413,6 +443,14 @@ def extra_configs(dev, w2):
         ms, _ = timed_launches(fn, 20)
         res[f"producer_{n}"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
                                 "bytes": nbytes}
+
+    log("[bench] decode-step linear layers")
+    for rows in (1, 128):
+        layer = {}
+        for name, fn, nbytes in linear_calls(dev, rows):
+            ms, _ = timed_launches(fn, 20)
+            layer[name] = {"us": round(ms * 1000, 2), "GB/s": round(nbytes / ms / 1e6, 1), "bytes": nbytes}
+        res[f"linear_{rows}rows"] = layer
 
     log("[bench] cfg4")
     w4 = make_workload("cfg4", dev)
