@@ -129,6 +129,32 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride,
                         pk_stream_t stream);
 
 /*
+ * pk_varlen_attention_ex -- pk_varlen_attention with a cache hint for the decode reads
+ * (no counterpart in the reference: flash_attn_varlen_func has no such argument).
+ * Decode K/V reads at key positions >= cached_prefix_keys use non-temporal (streaming)
+ * loads, earlier ones normal loads, decided per split of split-K work by its first key;
+ * cached_prefix_keys < 0 reads every key with normal loads. Prefix caching only ever
+ * shares a sequence's leading blocks, so a caller sets this to the longest prefix its
+ * block manager may share (0 when blocks are never shared between sequences).
+ * pk_varlen_attention uses PK_CACHED_PREFIX_KEYS_DEFAULT. The hint never changes results.
+ */
+#define PK_CACHED_PREFIX_KEYS_DEFAULT 2048
+
+int pk_varlen_attention_ex(const void* q, int64_t q_row_stride,
+                           const void* k, const void* v,
+                           int64_t k_row_stride, int64_t v_row_stride,
+                           int64_t k_block_stride, int64_t v_block_stride,
+                           const int32_t* block_table, int32_t block_table_stride,
+                           int32_t block_size,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                           int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                           float softmax_scale, int32_t causal,
+                           void* out, int64_t out_row_stride,
+                           void* workspace, size_t workspace_bytes,
+                           int32_t cached_prefix_keys, pk_stream_t stream);
+
+/*
  * Bytes of workspace pk_varlen_attention needs for these launch bounds: the
  * split-K partial outputs of the decode kernel (none when every sequence fits
  * one split) and, when max_seqlen_q > 1, the prefill work plan (work list,

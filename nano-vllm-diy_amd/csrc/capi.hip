@@ -115,7 +115,7 @@ int check_linear(const char* what, const void* x, int64_t x_row_stride, const vo
 
 extern "C" {
 
-int pk_abi_version(void) { return 4; }
+int pk_abi_version(void) { return 5; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -183,6 +183,22 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
                         int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
                         int32_t causal, void* out, int64_t out_row_stride, void* workspace,
                         size_t workspace_bytes, pk_stream_t stream) {
+  return pk_varlen_attention_ex(q, q_row_stride, k, v, k_row_stride, v_row_stride, k_block_stride,
+                                v_block_stride, block_table, block_table_stride, block_size, cu_seqlens_q,
+                                cu_seqlens_k, num_seqs, max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads,
+                                head_dim, softmax_scale, causal, out, out_row_stride, workspace,
+                                workspace_bytes, PK_CACHED_PREFIX_KEYS_DEFAULT, stream);
+}
+
+int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, const void* v,
+                           int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                           int64_t v_block_stride, const int32_t* block_table,
+                           int32_t block_table_stride, int32_t block_size,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                           int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+                           int32_t causal, void* out, int64_t out_row_stride, void* workspace,
+                           size_t workspace_bytes, int32_t cached_prefix_keys, pk_stream_t stream) {
   g_last_error.clear();
   if (head_dim != pk::kHeadDim)
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: head_dim=%d not built (only %d)", head_dim, pk::kHeadDim);
@@ -265,6 +281,7 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.out = static_cast<uint16_t*>(out);
   a.out_row_stride = out_row_stride;
+  a.stream_from = cached_prefix_keys;
   a.split_tokens = ws.split_tokens;
   a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
   char* const wsb = static_cast<char*>(workspace);

@@ -43,14 +43,6 @@ namespace {
 #ifndef PK_DECODE_MIN_SPLIT
 #define PK_DECODE_MIN_SPLIT 64     // shortest split (keys) the sizing goes down to
 #endif
-#ifndef PK_DECODE_NT_FROM
-// Keys at positions >= PK_DECODE_NT_FROM are read with non-temporal (streaming) loads,
-// earlier ones with normal loads. Prefix caching can only share a sequence's leading
-// blocks, so those are the reads worth keeping in L2 / Infinity Cache; everything past
-// them is read once per step and only displaces useful lines. The choice is made per
-// split (by its first key), so keep this a multiple of the split size. -1: never stream.
-#define PK_DECODE_NT_FROM 2048
-#endif
 
 constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
 
@@ -264,7 +256,11 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
     for (int e = 0; e < 8; ++e) st.acc[i][e] = 0.f;
   }
 
-  const bool stream = PK_DECODE_NT_FROM >= 0 && t_begin >= PK_DECODE_NT_FROM;  // per work-group
+  // Keys at positions >= a.stream_from are read with non-temporal (streaming) loads, earlier
+  // ones with normal loads: prefix caching can only share a sequence's leading blocks, so
+  // those are the reads worth keeping in L2 / Infinity Cache; everything past them is read
+  // once per step and only displaces useful lines. Decided per split (by its first key).
+  const bool stream = a.stream_from >= 0 && t_begin >= a.stream_from;
   if (stream)
     decode_range<G, U, PAGED, true>(st, a, lane_bytes, b, k0, t_begin, t_end);
   else

@@ -41,6 +41,12 @@ SIGNATURES = {
         _c_void_p, _i64,                    # out, out_row_stride
         _c_void_p, _size_t,                 # workspace, workspace_bytes
         _c_void_p]),                        # stream
+    "pk_varlen_attention_ex": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+        _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
+        _i32, _i32, _i32, ctypes.c_float, _i32, _c_void_p, _i64, _c_void_p, _size_t,
+        _i32,                               # cached_prefix_keys
+        _c_void_p]),                        # stream
     "pk_varlen_attention_workspace_bytes": (_size_t, [_i32, _i32, _i32, _i32, _i32]),
     "pk_gather_kv": (ctypes.c_int, [
         _c_void_p, _i64, _i32, _c_void_p, _i32, _c_void_p, _i32, _i32, _i32, _c_void_p,
@@ -74,7 +80,7 @@ SIGNATURES = {
         _c_void_p, _size_t, _c_void_p]),    # workspace, workspace_bytes, stream
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -107,7 +107,8 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      max_seqlen_q: int, max_seqlen_k: int,
                      softmax_scale: float | None = None, causal: bool = True,
                      block_table: torch.Tensor | None = None,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None,
+                     cached_prefix_keys: int | None = None) -> torch.Tensor:
     """Causal varlen attention with optional paged K/V; bf16 in and out.
 
     Same arguments and meaning as the flash_attn_varlen_func call of the reference
@@ -116,6 +117,11 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     (S, W) int32; per-sequence lengths from cu_seqlens_q / cu_seqlens_k (S + 1,)
     int32; bottom-right-aligned causal mask; GQA h -> h // (Hq / Hkv).
     Returns out (Nq, Hq, D) bf16.
+
+    cached_prefix_keys (an addition, results unchanged): decode keys from this position on
+    are read with streaming loads, earlier ones kept in cache -- the longest prefix the
+    caller's block manager may share between sequences (0: none shared, -1: cache every
+    read). None keeps the library default (PK_CACHED_PREFIX_KEYS_DEFAULT = 2048).
     """
     nq, num_heads, head_dim = q.shape
     dev = q.device
@@ -165,17 +171,19 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
     nbytes = workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k)
     ws = _workspace(nbytes, dev)
-    check(lib().pk_varlen_attention(
-        q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(),
-        k_row, v_row, k_blk, v_blk,
-        bt_ptr, bt_stride, block_size,
-        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
-        num_seqs, int(max_seqlen_q), int(max_seqlen_k),
-        num_heads, num_kv_heads, head_dim,
-        scale, 1 if causal else 0,
-        out.data_ptr(), out.stride(0),
-        ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
-        _stream(q)), "pk_varlen_attention")
+    args = (q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(),
+            k_row, v_row, k_blk, v_blk,
+            bt_ptr, bt_stride, block_size,
+            cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(),
+            num_seqs, int(max_seqlen_q), int(max_seqlen_k),
+            num_heads, num_kv_heads, head_dim,
+            scale, 1 if causal else 0,
+            out.data_ptr(), out.stride(0),
+            ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0)
+    if cached_prefix_keys is None:
+        check(lib().pk_varlen_attention(*args, _stream(q)), "pk_varlen_attention")
+    else:
+        check(lib().pk_varlen_attention_ex(*args, int(cached_prefix_keys), _stream(q)), "pk_varlen_attention_ex")
     return out
 
 

@@ -118,9 +118,11 @@ class Qwen3Model:
                 o = ops.varlen_attention(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
                                          ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True)
             else:
+                # this engine has no prefix cache: no block is shared between sequences, so
+                # every decode read streams (cached_prefix_keys=0)
                 o = ops.varlen_attention(q, kc, vc, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
                                          ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True,
-                                         ctx.block_tables)
+                                         ctx.block_tables, cached_prefix_keys=0)
             if small:
                 x, residual = ops.linear_add_rmsnorm(o.view(-1, Hq * D), L["o"], residual,
                                                      L["post_norm"], eps, residual_out=residual)

@@ -367,3 +367,20 @@ def test_long_context_small_batch(gpu):
     want = oracle.varlen_attention(q.cpu(), kc.cpu(), vc.cpu(), cu_q, cu_k, None, True, bt)
     torch.cuda.synchronize()
     assert_close_bf16(out, want, "long context")
+
+
+@pytest.mark.parametrize("name,num_seqs", [("cfg2", 24), ("cfg3", 12), ("cfg4", 16)])
+def test_cache_hint_never_changes_results(gpu, name, num_seqs):
+    """pk_varlen_attention_ex's cached_prefix_keys only picks the load flavour (normal or
+    streaming) per decode split: outputs are bit-identical to the default entry point for
+    every value, including streaming all keys (0) and none (-1)."""
+    w = make_workload(name, gpu, num_seqs=num_seqs)
+    pagedkv.store_kvcache(w.k, w.v, w.k_cache, w.v_cache, w.slot_mapping)
+    args = (w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k, w.max_seqlen_q,
+            w.max_seqlen_k, 128 ** -0.5, True, w.block_tables)
+    print(f"[cache_hint] {name} seqs={num_seqs}", flush=True)
+    ref = pagedkv.varlen_attention(*args)
+    outs = [pagedkv.varlen_attention(*args, cached_prefix_keys=c) for c in (0, -1, 256, 2048, 1 << 20)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert bits_equal(o, ref)
