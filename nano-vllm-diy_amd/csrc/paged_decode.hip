@@ -293,8 +293,8 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
 // "last work-group merges" tail in the split kernel) because the XCD L2 caches are not
 // coherent with each other: a device-scope fence per work-group would write back and
 // invalidate a whole L2, while the kernel boundary makes every partial visible for free.
-// The split maxima and weights are computed in parallel across splits (block reductions),
-// then thread d forms the weighted sum of element d with four independent accumulators.
+// Up to kCombineFast splits are merged from registers in two dependent memory round trips
+// (the sequence's lengths, then all partials at once); longer contexts take the LDS path.
 constexpr int kCombineThreads = kHeadDim;  // thread d owns output element d
 constexpr int kCombineMaxSplits = 256;     // splits per sequence the weight table holds
 
@@ -312,6 +312,8 @@ __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) 
   return v;
 }
 
+constexpr int kCombineFast = 16;           // splits merged from registers, without LDS
+
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const AttnArgs a) {
   constexpr int D = kHeadDim;
   __shared__ float w_s[kCombineMaxSplits];
@@ -319,13 +321,45 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int q0 = a.cu_q[b];
-  if (a.cu_q[b + 1] - q0 != 1) return;
-  const int Lk = min(a.cu_k[b + 1] - a.cu_k[b], a.max_seqlen_k);
+  const int q1 = a.cu_q[b + 1];
+  const int k_lo = a.cu_k[b];
+  const int k_hi = a.cu_k[b + 1];
+  if (q1 - q0 != 1) return;
+  const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
   if (Lk <= 0) return;
   const int nsplit = (Lk + a.split_tokens - 1) / a.split_tokens;
   if (nsplit <= 1) return;  // written directly by the split kernel
   const int H = a.num_heads;
   const int64_t unit0 = (int64_t)b * a.max_splits * H + h;  // partial of split j: unit0 + j H
+  const int d = threadIdx.x;
+  const float* po = a.part_o + unit0 * D + d;
+  const int64_t stride = (int64_t)H * D;
+  if (nsplit <= kCombineFast) {
+    // Every load of the merge is issued at once: lane j < nsplit of each wavefront reads
+    // split j's (max, sum), thread d element d of every split. The weights are formed in
+    // lanes 0..15 (16-lane reductions) and broadcast by shuffles: no LDS, no barrier.
+    const int lane = threadIdx.x & (kWave - 1);
+    float2 ml = make_float2(-INFINITY, 0.f);
+    if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)lane * H) * 2);
+    float v[kCombineFast];
+#pragma unroll
+    for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[(int64_t)j * stride] : 0.f;
+    float mx = ml.x;
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) mx = fmaxf(mx, xor_shfl(mx, m));
+    const float w = lane < nsplit ? exp2_fast(ml.x - mx) : 0.f;
+    float ls = w * ml.y;
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) ls += xor_shfl(ls, m);
+    const float lsum = __shfl(ls, 0, kWave);
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kCombineFast; ++j) acc = fmaf(__shfl(w, j, kWave), v[j], acc);
+    a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(acc / lsum);
+    return;
+  }
+  // Long contexts: split maxima and weights by block reductions into LDS, then thread d
+  // forms the weighted sum of element d with four independent accumulators.
   float mx = -INFINITY;
   for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) mx = fmaxf(mx, a.part_ml[(unit0 + (int64_t)j * H) * 2]);
   mx = block_reduce(mx, true, red);
@@ -337,9 +371,6 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
     lsum = fmaf(w, ml.y, lsum);
   }
   lsum = block_reduce(lsum, false, red);  // its barriers also publish w_s
-  const int d = threadIdx.x;
-  const float* po = a.part_o + unit0 * D + d;
-  const int64_t stride = (int64_t)H * D;
   float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
   int j = 0;
   for (; j + 4 <= nsplit; j += 4) {
