@@ -61,8 +61,15 @@ constexpr int kTileBytes = kTileKeys * kRowBytes;        // 16 KiB per operand p
 constexpr int kPlanThreads = 1024;     // plan work-group
 constexpr int kPlanCache = 2048;       // sequences whose lengths the plan keeps in LDS
 constexpr int kMinSplitTiles = 8;      // never split a unit's keys below 512 per item
+#ifndef PK_PREFILL_SPLIT_NUM
+#define PK_PREFILL_SPLIT_NUM 2
+#define PK_PREFILL_SPLIT_DEN 3
+#endif
+constexpr int kSplitNum = PK_PREFILL_SPLIT_NUM;  // split size = kSplitNum / kSplitDen x work per slot
+constexpr int kSplitDen = PK_PREFILL_SPLIT_DEN;
 constexpr int kMergeThreads = 256;     // merge: thread = row of the unit
 constexpr int kMergeGroups = 1024;
+constexpr int kMergeBatch = 8;         // merge: splits whose (max, sum) load in one batch
 constexpr int kBuckets = 4;            // length buckets of the work list (longest first)
 constexpr float kLazyLog2 = 8.f;       // reference max moves only when exceeded by 2^8
 
@@ -405,9 +412,11 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const AttnAr
 #pragma unroll
   for (int w = 0; w < W; ++w) work += red[w];
   work *= hkv;
-  // split size: 1.5 groups of work per slot, at least kMinSplitTiles (no unit has 2^20 tiles)
+  // split size: kSplitNum / kSplitDen of the work per slot, at least kMinSplitTiles (no unit
+  // has 2^20 tiles)
   const int T = (int)min((long long)(1 << 20),
-                         max((long long)kMinSplitTiles, (2 * (work / 3) + a.pf_slots - 1) / a.pf_slots + 1));
+                         max((long long)kMinSplitTiles,
+                             (kSplitNum * (work / kSplitDen) + a.pf_slots - 1) / a.pf_slots + 1));
 
   // pass 2: groups per length bucket
   for (int b = wave; b < S; b += W) {
@@ -677,24 +686,35 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
     const int h = g * G + r / TM;
     if (tok >= Lq) continue;
     if ((pg + n) * hkv > a.pf_part_cap) continue;  // cannot happen: the plan bounds partial ids
-    // two passes over the splits: running max, then weights and numerators; every pass
-    // issues all of a split's loads before using them
+    // (max, sum) of the first kMergeBatch splits in one batch of loads; then the numerators,
+    // the loads of split s + 1 in flight while split s is accumulated
+    const float* ml_base = a.pf_part_ml + ((int64_t)(pg * hkv + g) * kPrefillRows + r) * 2;
+    const int64_t ml_step = (int64_t)hkv * kPrefillRows * 2;  // next split of the unit
+    float2 ml[kMergeBatch];
+#pragma unroll
+    for (int s2 = 0; s2 < kMergeBatch; ++s2)
+      ml[s2] = s2 < n ? *reinterpret_cast<const float2*>(ml_base + s2 * ml_step) : make_float2(-INFINITY, 0.f);
     float M = -INFINITY;
-    for (int s = 0; s < n; ++s) M = fmaxf(M, a.pf_part_ml[((int64_t)((pg + s) * hkv + g) * kPrefillRows + r) * 2]);
+#pragma unroll
+    for (int s2 = 0; s2 < kMergeBatch; ++s2) M = fmaxf(M, ml[s2].x);
+    for (int s2 = kMergeBatch; s2 < n; ++s2) M = fmaxf(M, ml_base[s2 * ml_step]);
     float4 acc[CQ];
 #pragma unroll
     for (int c = 0; c < CQ; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.f;
     if (M != -INFINITY) {
-      for (int s = 0; s < n; ++s) {
-        const int p = (pg + s) * hkv + g;
-        const float* po = a.pf_part_o + (int64_t)p * (32 * kPrefillRows * 4);
-        f32x4 v[CQ];
+      const int64_t po_step = (int64_t)hkv * (32 * kPrefillRows * 4);
+      const float* po_base = a.pf_part_o + (int64_t)(pg * hkv + g) * (32 * kPrefillRows * 4) +
+                             ((int64_t)c0 * kPrefillRows + r) * 4;
+      const auto load = [&](int s2, f32x4 (&v)[CQ]) {
 #pragma unroll
-        for (int c = 0; c < CQ; ++c) v[c] = *reinterpret_cast<const f32x4*>(po + ((int64_t)(c0 + c) * kPrefillRows + r) * 4);
-        const float2 ml = *reinterpret_cast<const float2*>(a.pf_part_ml + ((int64_t)p * kPrefillRows + r) * 2);
-        const float wgt = exp2_fast(ml.x - M);  // 0 for a split whose rows saw no key
-        L += wgt * ml.y;
+        for (int c = 0; c < CQ; ++c)
+          v[c] = *reinterpret_cast<const f32x4*>(po_base + s2 * po_step + (int64_t)c * kPrefillRows * 4);
+      };
+      const auto add = [&](int s2, const f32x4 (&v)[CQ]) {
+        const float2 m = s2 < kMergeBatch ? ml[s2] : *reinterpret_cast<const float2*>(ml_base + s2 * ml_step);
+        const float wgt = exp2_fast(m.x - M);  // 0 for a split whose rows saw no key
+        L += wgt * m.y;
 #pragma unroll
         for (int c = 0; c < CQ; ++c) {
           acc[c].x += wgt * v[c][0];
@@ -702,6 +722,15 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
           acc[c].z += wgt * v[c][2];
           acc[c].w += wgt * v[c][3];
         }
+      };
+      f32x4 va[CQ], vb[CQ];
+      load(0, va);
+      for (int s2 = 0; s2 < n; s2 += 2) {
+        if (s2 + 1 < n) load(s2 + 1, vb);
+        add(s2, va);
+        if (s2 + 1 >= n) break;
+        if (s2 + 2 < n) load(s2 + 2, va);
+        add(s2 + 1, vb);
       }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
