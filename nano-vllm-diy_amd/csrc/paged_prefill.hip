@@ -484,8 +484,12 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
   const int tb = it.z & 0xffff;
   const int te = it.z >> 16;
   const int part = it.w < 0 ? -1 : it.w * a.num_kv_heads + g;
+  // The work list is trusted only as far as the buffers reach: an entry naming a sequence or
+  // key tiles outside this call (a workspace overwritten by an overlapping call) is skipped.
+  if (b < 0 || b >= a.num_seqs) return;
   const SeqDims sd = seq_dims<TM>(a, b);
   const int q0 = sd.q0, Lq = sd.Lq, k0 = sd.k0, Lk = sd.Lk, P = sd.P;
+  if (tb > te || te > (Lk + TN - 1) / TN) return;
   const int tok_begin = qt * TM;
 
   const int col = lane & 31;   // MFMA column = this lane's query row inside a block
@@ -626,7 +630,7 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel
   // blockIdx mod 8 first (items i = 8 j + x), then the others in turn. Every claim moves a
   // counter forward, and a work-group leaves once all eight sub-queues are exhausted.
   const int xcd = blockIdx.x & 7;
-  const int num_items = a.pf_queue[8];
+  const int num_items = (int)min((int64_t)a.pf_queue[8], (int64_t)a.pf_item_cap * a.num_kv_heads);
   int sq = 0;
   for (int it = 0;; it ^= 1) {
     if (tid == 0) {
@@ -664,7 +668,7 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
   constexpr int D = kHeadDim;
   constexpr int TM = kPrefillRows / G;
   constexpr int CQ = 8;  // chunks per quarter
-  const int nw = a.pf_queue[9] * 4;
+  const int nw = (int)min((int64_t)a.pf_queue[9], (int64_t)a.pf_merge_cap * a.num_kv_heads) * 4;
   const int r = threadIdx.x;
   const int hkv = a.num_kv_heads;
   // w = (unit, quarter) * hkv + g: with 8 kv heads, head g's merges run on XCD g (work-groups
@@ -680,12 +684,13 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
     const int qt = e.y;
     const int pg = e.z;
     const int n = e.w;
+    if (b < 0 || b >= a.num_seqs || pg < 0 || n <= 0) continue;  // see prefill_item
     const int q0 = a.cu_q[b];
     const int Lq = a.cu_q[b + 1] - q0;
     const int tok = qt * TM + r % TM;
     const int h = g * G + r / TM;
     if (tok >= Lq) continue;
-    if ((pg + n) * hkv > a.pf_part_cap) continue;  // cannot happen: the plan bounds partial ids
+    if ((int64_t)(pg + n) * hkv > a.pf_part_cap) continue;  // the plan bounds partial ids
     // (max, sum) of the first kMergeBatch splits in one batch of loads; then the numerators,
     // the loads of split s + 1 in flight while split s is accumulated
     const float* ml_base = a.pf_part_ml + ((int64_t)(pg * hkv + g) * kPrefillRows + r) * 2;

@@ -12,7 +12,7 @@ import torch
 
 from ._lib import check, lib
 
-_workspaces: dict[int, torch.Tensor] = {}  # device index -> cached workspace
+_workspaces: dict[int, torch.Tensor] = {}  # device index -> workspace of graph-captured calls
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -77,29 +77,47 @@ def workspace_bytes(num_seqs: int, num_heads: int, head_dim: int, max_seqlen_q: 
 
 def _workspace(nbytes: int, device: torch.device,
                cache: dict[int, torch.Tensor] = _workspaces) -> torch.Tensor | None:
-    """Per-device scratch, grown outside graph capture and reused afterwards.
+    """Scratch for one call.
 
-    Under capture a too-small cached buffer is not replaced (that would free memory a
-    recorded graph may still use); a private buffer from the capture pool is used. Calls
-    on different streams of one device must not overlap while they share this buffer.
+    Outside graph capture every call takes its own buffer from torch's caching allocator,
+    which orders reuse by stream, so calls on different streams may overlap. Under capture
+    the buffer reserved ahead of it (reserve_workspace / reserve_linear_workspace) is used
+    when it is large enough, so all graphs of a device share one buffer instead of holding
+    one each; graphs sharing it must not replay concurrently (the rule for torch's shared
+    graph memory pools). Without a large enough reservation a buffer from the capture pool
+    is used.
     """
     if nbytes == 0:
         return None
+    if torch.cuda.is_current_stream_capturing():
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        ws = cache.get(idx)
+        if ws is not None and ws.numel() >= nbytes:
+            return ws
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def _given_workspace(ws: torch.Tensor, nbytes: int, device: torch.device) -> torch.Tensor:
+    if ws.dtype != torch.uint8 or ws.device != device or not ws.is_contiguous() or ws.numel() < nbytes:
+        raise ValueError(f"workspace must be a contiguous uint8 tensor of >= {nbytes} bytes on {device}")
+    return ws
+
+
+def _reserve(nbytes: int, device: torch.device, cache: dict[int, torch.Tensor]) -> None:
+    """Grow the per-device buffer that captured calls use (outside capture only)."""
+    if nbytes == 0 or torch.cuda.is_current_stream_capturing():
+        return
     idx = device.index if device.index is not None else torch.cuda.current_device()
     ws = cache.get(idx)
-    if ws is not None and ws.numel() >= nbytes:
-        return ws
-    fresh = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    if not torch.cuda.is_current_stream_capturing():
-        cache[idx] = fresh
-    return fresh
+    if ws is None or ws.numel() < nbytes:
+        cache[idx] = torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def reserve_workspace(num_seqs: int, num_heads: int, head_dim: int, max_seqlen_q: int,
                       max_seqlen_k: int, device: torch.device | str = "cuda") -> None:
-    """Grow the cached workspace ahead of graph capture (call outside capture)."""
-    _workspace(workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k),
-               torch.device(device))
+    """Reserve the workspace that graph-captured attention calls use (call before capture)."""
+    _reserve(workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k),
+             torch.device(device), _workspaces)
 
 
 def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -108,7 +126,8 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      softmax_scale: float | None = None, causal: bool = True,
                      block_table: torch.Tensor | None = None,
                      out: torch.Tensor | None = None,
-                     cached_prefix_keys: int | None = None) -> torch.Tensor:
+                     cached_prefix_keys: int | None = None,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Causal varlen attention with optional paged K/V; bf16 in and out.
 
     Same arguments and meaning as the flash_attn_varlen_func call of the reference
@@ -122,6 +141,8 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     are read with streaming loads, earlier ones kept in cache -- the longest prefix the
     caller's block manager may share between sequences (0: none shared, -1: cache every
     read). None keeps the library default (PK_CACHED_PREFIX_KEYS_DEFAULT = 2048).
+    workspace: caller-owned uint8 scratch of at least workspace_bytes(...) bytes (as the
+    C-ABI takes it); None takes one per call (or the reserved one under graph capture).
     """
     nq, num_heads, head_dim = q.shape
     dev = q.device
@@ -170,7 +191,7 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("out must be (Nq, Hq, D) bf16 with contiguous heads")
     scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
     nbytes = workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k)
-    ws = _workspace(nbytes, dev)
+    ws = _workspace(nbytes, dev) if workspace is None else _given_workspace(workspace, nbytes, dev)
     args = (q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(),
             k_row, v_row, k_blk, v_blk,
             bt_ptr, bt_stride, block_size,
@@ -382,7 +403,7 @@ def lm_head_greedy(hidden_states: torch.Tensor, weight: torch.Tensor,
 # ----------------------------------------------------------- decode-step linear layers ---
 LINEAR_MAX_ROWS = 128
 LINEAR_STORE, LINEAR_SILU_MUL, LINEAR_ADD_RMSNORM = 0, 1, 2
-_lin_workspaces: dict[int, torch.Tensor] = {}  # device index -> cached linear-layer scratch
+_lin_workspaces: dict[int, torch.Tensor] = {}  # device index -> scratch of graph-captured calls
 
 
 def linear_workspace_bytes(rows: int, n_out: int, k: int, epilogue: int = LINEAR_STORE) -> int:
@@ -391,8 +412,8 @@ def linear_workspace_bytes(rows: int, n_out: int, k: int, epilogue: int = LINEAR
 
 
 def reserve_linear_workspace(nbytes: int, device: torch.device | str = "cuda") -> None:
-    """Grow the cached linear-layer scratch ahead of graph capture (call outside capture)."""
-    _workspace(nbytes, torch.device(device), _lin_workspaces)
+    """Reserve the scratch that graph-captured linear-layer calls use (call before capture)."""
+    _reserve(nbytes, torch.device(device), _lin_workspaces)
 
 
 def _linear_args(x: torch.Tensor, weight: torch.Tensor, rows_per_out: int):
@@ -406,9 +427,10 @@ def _linear_args(x: torch.Tensor, weight: torch.Tensor, rows_per_out: int):
     return rows, k, weight.shape[0] // rows_per_out
 
 
-def _linear_call(x, weight, rows, k, n_out, epilogue, out):
+def _linear_call(x, weight, rows, k, n_out, epilogue, out, workspace=None):
     nbytes = linear_workspace_bytes(rows, n_out, k, epilogue)
-    ws = _workspace(nbytes, x.device, _lin_workspaces)
+    ws = _workspace(nbytes, x.device, _lin_workspaces) if workspace is None else \
+        _given_workspace(workspace, nbytes, x.device)
     check(lib().pk_linear(
         x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n_out, k, epilogue,
         out.data_ptr(), out.stride(0), ws.data_ptr() if ws is not None else 0, nbytes,
@@ -416,22 +438,25 @@ def _linear_call(x, weight, rows, k, n_out, epilogue, out):
     return out
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+           workspace: torch.Tensor | None = None) -> torch.Tensor:
     """F.linear(x, weight) of a decode step (src/layers/linear.py:74-75, :169-170): bf16
-    (rows <= 128, k) x (n_out, k)^T with fp32 accumulation, rounded to bf16."""
+    (rows <= 128, k) x (n_out, k)^T with fp32 accumulation, rounded to bf16. workspace:
+    optional caller-owned uint8 scratch of linear_workspace_bytes(...) bytes."""
     rows, k, n_out = _linear_args(x, weight, 1)
     if out is None:
         out = torch.empty(rows, n_out, dtype=torch.bfloat16, device=x.device)
-    return _linear_call(x, weight, rows, k, n_out, LINEAR_STORE, out)
+    return _linear_call(x, weight, rows, k, n_out, LINEAR_STORE, out, workspace)
 
 
-def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
     """SiluAndMul(F.linear(x, weight)) for the merged gate/up weight (2 inter, k)
     (qwen3.py:120-121): gate and up outputs are rounded to bf16, then silu(g) * u in fp32."""
     rows, k, inter = _linear_args(x, weight, 2)
     if out is None:
         out = torch.empty(rows, inter, dtype=torch.bfloat16, device=x.device)
-    return _linear_call(x, weight, rows, k, inter, LINEAR_SILU_MUL, out)
+    return _linear_call(x, weight, rows, k, inter, LINEAR_SILU_MUL, out, workspace)
 
 
 def linear_add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,

@@ -322,25 +322,58 @@ def test_graph_capture_padded_decode_replay(gpu):
 
 
 def test_workspace_reuse_across_batch_shapes(gpu):
-    """One cached workspace serves calls of different shapes in any order: each result is
+    """One shared workspace serves calls of different shapes in any order: each result is
     bit-identical to the same call on a fresh (zero-filled) workspace."""
-    import pagedkv.ops as ops
     shapes = [("cfg4", 16), ("cfg2", 24), ("cfg3", None), ("cfg1_decode", None), ("cfg2", 8), ("cfg3", 40)]
     wls = [make_workload(n, gpu, num_seqs=s) for n, s in shapes]
 
-    def run(w):
+    def need(w):
+        return pagedkv.workspace_bytes(len(w.q_lens), 16, 128, w.max_seqlen_q, w.max_seqlen_k)
+
+    def run(w, ws):
         return pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k,
-                                        w.max_seqlen_q, w.max_seqlen_k, None, True, w.block_tables)
-    fresh = []
-    for w in wls:
-        ops._workspaces.clear()
-        fresh.append(run(w))
-    ops._workspaces.clear()
+                                        w.max_seqlen_q, w.max_seqlen_k, None, True, w.block_tables,
+                                        workspace=ws)
+    fresh = [run(w, torch.zeros(max(1, need(w)), dtype=torch.uint8, device=gpu)) for w in wls]
+    shared = torch.empty(max(need(w) for w in wls), dtype=torch.uint8, device=gpu)
     for rep in range(2):
         for w, want in zip(wls, fresh):
-            got = run(w)
+            got = run(w, shared)
             torch.cuda.synchronize()
             assert bits_equal(got, want), f"{w.name} rep {rep}"
+
+
+def test_calls_on_two_streams_may_overlap(gpu):
+    """Without an explicit workspace every call takes its own scratch, so a decode batch and
+    a prefill batch may run concurrently on two streams (one shared per-device buffer would
+    let the decode partials overwrite the prefill work list)."""
+    w = make_workload("cfg3", gpu, num_seqs=24)
+    dec = [i for i, lq in enumerate(w.q_lens) if lq == 1]
+    pre = [i for i, lq in enumerate(w.q_lens) if lq > 1]
+
+    def sub(ids):
+        cu_q = w.cu_seqlens_q.cpu().tolist()
+        rows = [r for i in ids for r in range(cu_q[i], cu_q[i + 1])]
+        q = w.q[torch.tensor(rows, device=gpu)]
+        lq = [w.q_lens[i] for i in ids]
+        lk = [w.k_lens[i] for i in ids]
+        cq = torch.tensor([0] + np.cumsum(lq).tolist(), dtype=torch.int32, device=gpu)
+        ck = torch.tensor([0] + np.cumsum(lk).tolist(), dtype=torch.int32, device=gpu)
+        bt = w.block_tables[torch.tensor(ids, device=gpu)].contiguous()
+        return lambda: pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cq, ck, max(lq), max(lk), None, True, bt)
+    fd, fp = sub(dec), sub(pre)
+    want_d, want_p = fd(), fp()
+    torch.cuda.synchronize()
+    print("[two streams] cfg3 decode + prefill sub-batches", flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    for _ in range(3):
+        got_d = fd()
+        with torch.cuda.stream(side):
+            got_p = fp()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        assert bits_equal(got_d, want_d) and bits_equal(got_p, want_p)
 
 
 def test_long_context_small_batch(gpu):

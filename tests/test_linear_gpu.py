@@ -140,15 +140,19 @@ def test_strided_rows(gpu):
 
 
 def test_deterministic_and_shared_workspace(gpu):
-    """Repeated calls are bit-identical, also when calls of other shapes reuse the scratch
-    in between."""
+    """Repeated calls are bit-identical, also when a call of another shape uses the same
+    scratch in between."""
     x = _rand((128, 1024), 21).to(gpu)
     w = _rand((2 * 3072, 1024), 22, 0.02).to(gpu)
-    a = pagedkv.linear_silu_mul(x, w)
-    pagedkv.linear(_rand((77, 3072), 23).to(gpu), _rand((1024, 3072), 24, 0.02).to(gpu))
-    b = pagedkv.linear_silu_mul(x, w)
+    x2, w2 = _rand((77, 3072), 23).to(gpu), _rand((1024, 3072), 24, 0.02).to(gpu)
+    nbytes = max(pagedkv.linear_workspace_bytes(128, 3072, 1024, 1), pagedkv.linear_workspace_bytes(77, 1024, 3072))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=gpu)
+    a = pagedkv.linear_silu_mul(x, w, workspace=ws)
+    pagedkv.linear(x2, w2, workspace=ws)
+    b = pagedkv.linear_silu_mul(x, w, workspace=ws)
+    c = pagedkv.linear_silu_mul(x, w)
     torch.cuda.synchronize()
-    assert _bits(a, b)
+    assert _bits(a, b) and _bits(a, c)
 
 
 def test_rejects_large_batches(gpu):

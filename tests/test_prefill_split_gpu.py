@@ -48,9 +48,19 @@ def _batch(dev, seqs, hq=16, hkv=8, seed=0, paged=True):
     return q, k, v, cu_q, cu_k, bt
 
 
-def _run(dev, q, k, v, cu_q, cu_k, bt, seqs, causal=True):
+def _ws_bytes(args, seqs):
+    q = args[0]
+    return pagedkv.workspace_bytes(len(seqs), q.shape[1], q.shape[2], max(s[0] for s in seqs),
+                                   max(s[1] for s in seqs))
+
+
+def _run(dev, q, k, v, cu_q, cu_k, bt, seqs, causal=True, workspace=None, fresh_workspace=False):
+    """fresh_workspace: a zero-filled workspace of exactly the needed size for this call."""
+    if fresh_workspace:
+        workspace = torch.zeros(max(1, _ws_bytes((q,), seqs)), dtype=torch.uint8, device=dev)
     return pagedkv.varlen_attention(q, k, v, cu_q.to(dev), cu_k.to(dev), max(s[0] for s in seqs),
-                                    max(s[1] for s in seqs), None, causal, None if bt is None else bt.to(dev))
+                                    max(s[1] for s in seqs), None, causal, None if bt is None else bt.to(dev),
+                                    workspace=workspace)
 
 
 def _check(dev, seqs, hq=16, hkv=8, paged=True, causal=True, seed=0, what=""):
@@ -104,19 +114,15 @@ def test_split_results_bit_identical_across_runs(gpu):
 
 
 def test_workspace_reuse_after_split_call(gpu):
-    """A split-heavy call, then small ones, then the split call again on one cached
-    workspace: every result equals the same call on a fresh workspace (the plan resets
-    its claim counters and rewrites its lists each call)."""
-    import pagedkv.ops as ops
+    """A split-heavy call, then small ones, then the split call again on one shared
+    workspace: every result equals the same call on a fresh zero-filled workspace (the plan
+    resets its claim counters and rewrites its lists each call)."""
     batches = [SKEWED, [(70, 70), (3, 900)], [(512, 512 + 4000)], SKEWED]
     args = [_batch(gpu, s, seed=11 + i) for i, s in enumerate(batches)]
-    fresh = []
-    for s, a in zip(batches, args):
-        ops._workspaces.clear()
-        fresh.append(_run(gpu, *a, s))
-    ops._workspaces.clear()
+    fresh = [_run(gpu, *a, s, fresh_workspace=True) for s, a in zip(batches, args)]
+    shared = torch.empty(max(_ws_bytes(a, s) for s, a in zip(batches, args)), dtype=torch.uint8, device=gpu)
     for rep in range(2):
         for s, a, want in zip(batches, args, fresh):
-            got = _run(gpu, *a, s)
+            got = _run(gpu, *a, s, workspace=shared)
             torch.cuda.synchronize()
             assert bits_equal(got, want), f"rep {rep} seqs {s}"
