@@ -84,10 +84,14 @@ def attention_call(w, sub=None):
 
     q, cu_q, cu_k, bt, mq, mk = (w.q, w.cu_seqlens_q, w.cu_seqlens_k, w.block_tables,
                                  w.max_seqlen_q, w.max_seqlen_k) if sub is None else sub
-    out = pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt)
+    # the batch's shared-prefix length from its block reference counts, as an engine passes it
+    hint = w.shared_prefix_keys
+    out = pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt,
+                                   cached_prefix_keys=hint)
 
     def fn():
-        pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt, out=out)
+        pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt, out=out,
+                                 cached_prefix_keys=hint)
     return fn
 
 
@@ -199,7 +203,8 @@ def main() -> int:
 
     def attend():
         pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
-                                 ctx.max_seqlen_q, ctx.max_seqlen_k, SCALE, True, ctx.block_tables, out=out)
+                                 ctx.max_seqlen_q, ctx.max_seqlen_k, SCALE, True, ctx.block_tables, out=out,
+                                 cached_prefix_keys=ctx.cached_prefix_keys)
 
     log(f"[bench] warmup {args.warmup} steps")
     for _ in range(args.warmup):
@@ -252,6 +257,7 @@ def main() -> int:
             "kv_bytes_per_step": kv_bytes,
             "store_bytes_per_step": store_bytes,
             "num_blocks": int(w.k_cache.shape[0]),
+            "cached_prefix_keys": ctx.cached_prefix_keys,
         },
         "roofline": {
             "bound": "hbm",
@@ -332,7 +338,8 @@ def pmc_probe(w) -> int:
     out = torch.empty_like(w.q)
     for _ in range(5):
         pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k, 1,
-                                 w.max_seqlen_k, SCALE, True, w.block_tables, out=out)
+                                 w.max_seqlen_k, SCALE, True, w.block_tables, out=out,
+                                 cached_prefix_keys=w.shared_prefix_keys)
     src = torch.ones(1 << 29, dtype=torch.int16, device=w.q.device)
     dst = torch.empty_like(src)
     for _ in range(5):

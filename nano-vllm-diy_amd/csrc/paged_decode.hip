@@ -46,12 +46,23 @@ namespace {
 
 constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
 
-__device__ __forceinline__ uint4 load16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through L2
 
-__device__ __forceinline__ uint4 load16_stream(const char* p) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(w.x, w.y, w.z, w.w);
+// Buffer resource over [base, base + bytes): raw addressing (stride 0), 32-bit dword format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes at base + row_off + lane_off: row_off is wave-uniform (scalar offset operand),
+// lane_off is the lane's column (one VGPR shared by every load of the step). STREAM sets the
+// non-temporal policy.
+template <bool STREAM>
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t row_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)lane_off, (int)row_off, STREAM ? 2 : 0);
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -76,12 +87,16 @@ struct DecodeState {
 // Issue the K then V loads of keys [t, t + U) of this lane's kv head. lane_bytes is the
 // lane's byte offset inside a token row. Keys past t_end re-read the step's last valid
 // row (same cache block, finite data) and consume() masks them to p = 0, so no load
-// needs a branch and all offsets past the wave-uniform base are the same per lane.
+// needs a branch. The loads are buffer loads over the step's U rows: the row offsets are
+// wave-uniform scalar operands and every load shares the lane-offset VGPR. (With
+// global loads each load needs its own vector address register, and at this kernel's
+// register pressure the compiler took those from the destinations of the previous step's
+// in-flight loads: the write-after-write wait then drained the pipeline every other step.)
 // STREAM selects non-temporal loads; it is a template parameter (not a runtime branch)
 // so the pipelined loop stays straight-line and its wait counts stay exact.
 template <int U, bool PAGED, bool STREAM>
 __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_bytes, int b, int k0, int t,
-                                            int t_end, uint4 (&kr)[U], uint4 (&vr)[U]) {
+                                            int t_end, u32x4 (&kr)[U], u32x4 (&vr)[U]) {
   const uint16_t* kp;
   const uint16_t* vp;
   if constexpr (PAGED) {
@@ -94,23 +109,16 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_byt
     kp = a.k + (int64_t)(k0 + t) * a.k_row_stride;
     vp = a.v + (int64_t)(k0 + t) * a.v_row_stride;
   }
-  // wave-uniform base + 32-bit per-lane offset: the scalar-base addressing form, no
-  // 64-bit vector address arithmetic (row strides are < 2^22 elements, checked on the host)
-  const char* kc = reinterpret_cast<const char*>(kp);
-  const char* vc = reinterpret_cast<const char*>(vp);
+  // row strides are < 2^22 elements (checked on the host), so U rows span < 2^27 bytes
   const uint32_t k_row_bytes = (uint32_t)a.k_row_stride * 2u;
   const uint32_t v_row_bytes = (uint32_t)a.v_row_stride * 2u;
+  const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, (uint32_t)U * k_row_bytes);
+  const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, (uint32_t)U * v_row_bytes);
   const int last = t_end - 1 - t;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const char* row = kc + (__umul24((uint32_t)min(u, last), k_row_bytes) + lane_bytes);
-    kr[u] = STREAM ? load16_stream(row) : load16(row);
-  }
+  for (int u = 0; u < U; ++u) kr[u] = load16<STREAM>(kr_rs, lane_bytes, __umul24((uint32_t)min(u, last), k_row_bytes));
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const char* row = vc + (__umul24((uint32_t)min(u, last), v_row_bytes) + lane_bytes);
-    vr[u] = STREAM ? load16_stream(row) : load16(row);
-  }
+  for (int u = 0; u < U; ++u) vr[u] = load16<STREAM>(vr_rs, lane_bytes, __umul24((uint32_t)min(u, last), v_row_bytes));
 }
 
 // Keys [t_begin, t_end) of one split through a two-stage software pipeline: the loads of
@@ -125,8 +133,8 @@ __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs&
 
 // Fold keys [t, t + U) (already loaded) into the running softmax state.
 template <int G, int U>
-__device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int t_end, const uint4 (&kr)[U],
-                                        const uint4 (&vr)[U]) {
+__device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int t_end, const u32x4 (&kr)[U],
+                                        const u32x4 (&vr)[U]) {
   // unscaled scores: 4 dot2 per (key, head) over this lane's 8 elements, then the
   // 16-lane DPP sum gives every lane of the row the full q.k of its key.
   float s[U][G];
@@ -193,7 +201,7 @@ template <int G, int U, bool PAGED, bool STREAM>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
                                              int k0, int t_begin, int t_end) {
   const float c2 = a.scale_log2;
-  uint4 kA[U], vA[U], kB[U], vB[U];
+  u32x4 kA[U], vA[U], kB[U], vB[U];
   issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
   for (int t = t_begin; t < t_end; t += 2 * U) {
     const int t1 = t + U;
@@ -267,6 +275,14 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
     decode_range<G, U, PAGED, false>(st, a, lane_bytes, b, k0, t_begin, t_end);
 
   if (!row_live) return;
+  // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous.
+  // They are written through to memory (sc1 stores) rather than left dirty in L2: the
+  // partial writes land in the middle of the K/V read stream, and measured on cfg2 (18.9 MB
+  // of partials against 4.8 GB of reads) write-back stores cost ~57 us of an 800 us call,
+  // write-through ~32 us, no writes at all 0.
+  const int64_t unit0 = ((int64_t)b * a.max_splits + split) * H;
+  const __amdgpu_buffer_rsrc_t po_rs = row_rsrc(a.part_o + unit0 * D, (uint32_t)(H * D * 4));
+  const __amdgpu_buffer_rsrc_t pml_rs = row_rsrc(a.part_ml + unit0 * 2, (uint32_t)(H * 8));
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int h = g * G + i;
@@ -279,12 +295,15 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
       w.w = pack_bf16x2(st.acc[i][6] * inv, st.acc[i][7] * inv);
       *reinterpret_cast<uint4*>(a.out + (int64_t)q0 * a.out_row_stride + h * D + c * 8) = w;
     } else {
-      const int64_t unit = ((int64_t)b * a.max_splits + split) * H + h;
-      float4* po = reinterpret_cast<float4*>(a.part_o + unit * D + c * 8);
-      po[0] = make_float4(st.acc[i][0], st.acc[i][1], st.acc[i][2], st.acc[i][3]);
-      po[1] = make_float4(st.acc[i][4], st.acc[i][5], st.acc[i][6], st.acc[i][7]);
-      // merged in the exp2 domain: store the scaled max
-      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + unit * 2) = make_float2(st.m[i] * c2, st.l[i]);
+      const int o = (h * D + c * 8) * 4;
+      const f32x4 lo = {st.acc[i][0], st.acc[i][1], st.acc[i][2], st.acc[i][3]};
+      const f32x4 hi = {st.acc[i][4], st.acc[i][5], st.acc[i][6], st.acc[i][7]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), po_rs, o, 0, kStoreThrough);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), po_rs, o + 16, 0, kStoreThrough);
+      if (c == 0) {  // merged in the exp2 domain: store the scaled max
+        const f32x2 ml = {st.m[i] * c2, st.l[i]};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ml), pml_rs, h * 8, 0, kStoreThrough);
+      }
     }
   }
 }

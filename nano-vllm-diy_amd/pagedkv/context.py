@@ -8,6 +8,9 @@ Context (src/utils/context.py:5-14), built by the runner (model_runner.py:174-23
 * context_lens: (S,) int32 key length per sequence; produced by the runner and,
   as in the reference, not read by Attention.
 * block_tables: (S, W) int32, -1 padded; None selects flat (fresh K/V) attention.
+* cached_prefix_keys (an addition; results never depend on it): the decode cache hint,
+  the longest prefix the batch's sequences share (shared_prefix_keys); None keeps the
+  library default.
 """
 from __future__ import annotations
 
@@ -26,3 +29,4 @@ class Context:
     slot_mapping: Tensor | None = None
     context_lens: Tensor | None = None
     block_tables: Tensor | None = None
+    cached_prefix_keys: int | None = None

@@ -8,6 +8,8 @@ them can run under torch.cuda.graph capture.
 """
 from __future__ import annotations
 
+from collections import Counter
+
 import torch
 
 from ._lib import check, lib
@@ -206,6 +208,25 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         check(lib().pk_varlen_attention_ex(*args, int(cached_prefix_keys), _stream(q)), "pk_varlen_attention_ex")
     return out
+
+
+def shared_prefix_keys(block_tables, block_size: int) -> int:
+    """The cached_prefix_keys value for a batch: the longest run of leading blocks that
+    some sequence shares with another (block reference count > 1, the count the
+    reference's block manager keeps, block_manager.py:141,149), in keys. Only leading
+    blocks can be shared (prefix hashes chain from the sequence start,
+    block_manager.py:96-181), so keys past this run are read once per step and can stream.
+    block_tables: per-sequence lists of block ids, or an (S, W) int tensor, -1 padded."""
+    if isinstance(block_tables, torch.Tensor):
+        block_tables = block_tables.cpu().tolist()
+    refs = Counter(b for row in block_tables for b in set(row) if b >= 0)
+    best = 0
+    for row in block_tables:
+        n = 0
+        while n < len(row) and row[n] >= 0 and refs[row[n]] > 1:
+            n += 1
+        best = max(best, n)
+    return best * block_size
 
 
 def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens_k: torch.Tensor,

@@ -66,7 +66,17 @@ class Workload:
             slot_mapping=self.slot_mapping,
             context_lens=self.context_lens,
             block_tables=self.block_tables,
+            cached_prefix_keys=self.shared_prefix_keys,
         )
+
+    @property
+    def shared_prefix_keys(self) -> int:
+        """Longest shared leading run of blocks, in keys (0 when no block is shared)."""
+        if "shared_prefix_keys" not in self.meta:
+            from .ops import shared_prefix_keys
+            self.meta["shared_prefix_keys"] = (0 if self.block_tables is None else
+                                               shared_prefix_keys(self.block_tables, BLOCK_SIZE))
+        return self.meta["shared_prefix_keys"]
 
     # ---- algorithmic work (per pass) ----
     def store_bytes(self) -> int:

@@ -236,3 +236,18 @@ def test_linear_workspace_sizes():
     assert f(64, 8192, 1024, 0) == 0
     assert f(128, 4096, 1024, 0) == 0
     assert f(64, 1024, 256, 2) == 64 * 1024 * 4
+
+
+def test_shared_prefix_keys_from_block_reference_counts():
+    from pagedkv import shared_prefix_keys
+    # two sequences share their first two blocks, a third shares nothing
+    assert shared_prefix_keys([[5, 6, 1], [5, 6, 2, 3], [7, 8]], 256) == 512
+    # sharing that does not start at the first block gives no cached prefix
+    assert shared_prefix_keys([[1, 9], [2, 9]], 256) == 0
+    # padding (-1) never counts, an all-shared table stops at its end
+    assert shared_prefix_keys(torch.tensor([[4, 5, -1], [4, 5, 6]], dtype=torch.int32), 16) == 32
+    assert shared_prefix_keys([], 256) == 0
+    # the seeded workloads: cfg4 shares its 2048-token prefix, cfg1 shares nothing
+    w4 = make_workload("cfg4")
+    assert w4.shared_prefix_keys == 2048 and w4.ctx.cached_prefix_keys == 2048
+    assert make_workload("cfg1_decode").shared_prefix_keys == 0
