@@ -43,6 +43,7 @@ struct AttnArgs {
   float* part_o;                // [num_seqs][max_splits][num_heads][head_dim]
   float* part_ml;               // [num_seqs][max_splits][num_heads][2] = (max, sum)
   int32_t stream_from;           // decode splits starting at key >= this use non-temporal loads (< 0: none)
+  int32_t store_through;         // decode partials written through L2 (set by the decode launch)
   int32_t split_tokens;
   int32_t max_splits;
   // chunked-prefill work plan (workspace): a work item is (sequence, kv head, query tile,

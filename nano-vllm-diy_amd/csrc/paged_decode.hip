@@ -51,6 +51,22 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through L2
+// Partial footprint (launch bound: sequences x splits x heads x D x 4 bytes) above which the
+// partials are written through L2. The eight XCD L2s hold 32 MB together: smaller partial
+// sets stay there, dirty, until the kernel ends; larger ones get evicted in the middle of the
+// K/V read stream, where write-back traffic is the costlier (measured: 256 sequences of
+// 1k-8k keys, 33.5 MB bound, 0.800 -> 0.778 ms with write-through; 128 sequences, 16.8 MB
+// bound, 114 -> 117 us, cfg3's decode part 221 -> 226 us).
+constexpr int64_t kStoreThroughBytes = 24ll << 20;
+
+template <int AUX>
+__device__ __forceinline__ void store_partial(const __amdgpu_buffer_rsrc_t& po_rs, const __amdgpu_buffer_rsrc_t& pml_rs,
+                                              int o, int ml_off, const f32x4& lo, const f32x4& hi, const f32x2& ml,
+                                              bool with_ml) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), po_rs, o, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), po_rs, o + 16, 0, AUX);
+  if (with_ml) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ml), pml_rs, ml_off, 0, AUX);
+}
 
 // Buffer resource over [base, base + bytes): raw addressing (stride 0), 32-bit dword format.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
@@ -275,11 +291,8 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
     decode_range<G, U, PAGED, false>(st, a, lane_bytes, b, k0, t_begin, t_end);
 
   if (!row_live) return;
-  // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous.
-  // They are written through to memory (sc1 stores) rather than left dirty in L2: the
-  // partial writes land in the middle of the K/V read stream, and measured on cfg2 (18.9 MB
-  // of partials against 4.8 GB of reads) write-back stores cost ~57 us of an 800 us call,
-  // write-through ~32 us, no writes at all 0.
+  // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous,
+  // written through L2 or left in it by the launch's choice (kStoreThroughBytes).
   const int64_t unit0 = ((int64_t)b * a.max_splits + split) * H;
   const __amdgpu_buffer_rsrc_t po_rs = row_rsrc(a.part_o + unit0 * D, (uint32_t)(H * D * 4));
   const __amdgpu_buffer_rsrc_t pml_rs = row_rsrc(a.part_ml + unit0 * 2, (uint32_t)(H * 8));
@@ -298,12 +311,11 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
       const int o = (h * D + c * 8) * 4;
       const f32x4 lo = {st.acc[i][0], st.acc[i][1], st.acc[i][2], st.acc[i][3]};
       const f32x4 hi = {st.acc[i][4], st.acc[i][5], st.acc[i][6], st.acc[i][7]};
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), po_rs, o, 0, kStoreThrough);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), po_rs, o + 16, 0, kStoreThrough);
-      if (c == 0) {  // merged in the exp2 domain: store the scaled max
-        const f32x2 ml = {st.m[i] * c2, st.l[i]};
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ml), pml_rs, h * 8, 0, kStoreThrough);
-      }
+      const f32x2 ml = {st.m[i] * c2, st.l[i]};  // merged in the exp2 domain: the scaled max
+      if (a.store_through)
+        store_partial<kStoreThrough>(po_rs, pml_rs, o, h * 8, lo, hi, ml, c == 0);
+      else
+        store_partial<0>(po_rs, pml_rs, o, h * 8, lo, hi, ml, c == 0);
     }
   }
 }
@@ -403,7 +415,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
 }
 
 template <int G, int U>
-hipError_t launch_decode_g(const AttnArgs& a, bool paged, hipStream_t stream) {
+hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
+  a.store_through = (int64_t)a.num_seqs * a.max_splits * a.num_heads * kHeadDim * 4 > kStoreThroughBytes;
   const int quads = (a.num_kv_heads + 3) / 4;   // wavefronts needed for all kv heads
   int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
   while (quads % waves != 0) --waves;            // no idle wavefront in any work-group
