@@ -59,12 +59,19 @@ constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through
 // bound, 114 -> 117 us, cfg3's decode part 221 -> 226 us).
 constexpr int64_t kStoreThroughBytes = 24ll << 20;
 
+// Slot of head_dim element d in a head's partial numerator row: lane c of the split kernel
+// holds elements 8c .. 8c + 7 and writes 8c .. 8c + 3 to slots 4c .. 4c + 3 and 8c + 4 ..
+// 8c + 7 to slots 64 + 4c .., so each of its two 16-byte stores covers 256 contiguous bytes
+// per head row. (Element order 8c .. 8c + 7 at slot 8c would leave every store instruction
+// writing every other 16 bytes: written through L2 that doubles the bytes that reach HBM.)
+__device__ __forceinline__ int partial_slot(int d) { return (d & 4 ? kHeadDim / 2 : 0) + (d >> 3) * 4 + (d & 3); }
+
 template <int AUX>
 __device__ __forceinline__ void store_partial(const __amdgpu_buffer_rsrc_t& po_rs, const __amdgpu_buffer_rsrc_t& pml_rs,
                                               int o, int ml_off, const f32x4& lo, const f32x4& hi, const f32x2& ml,
                                               bool with_ml) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), po_rs, o, 0, AUX);
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), po_rs, o + 16, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), po_rs, o + kHeadDim * 2, 0, AUX);
   if (with_ml) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ml), pml_rs, ml_off, 0, AUX);
 }
 
@@ -308,7 +315,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
       w.w = pack_bf16x2(st.acc[i][6] * inv, st.acc[i][7] * inv);
       *reinterpret_cast<uint4*>(a.out + (int64_t)q0 * a.out_row_stride + h * D + c * 8) = w;
     } else {
-      const int o = (h * D + c * 8) * 4;
+      const int o = (h * D + c * 4) * 4;  // partial_slot(8c .. 8c + 3) = 4c: see partial_slot
       const f32x4 lo = {st.acc[i][0], st.acc[i][1], st.acc[i][2], st.acc[i][3]};
       const f32x4 hi = {st.acc[i][4], st.acc[i][5], st.acc[i][6], st.acc[i][7]};
       const f32x2 ml = {st.m[i] * c2, st.l[i]};  // merged in the exp2 domain: the scaled max
@@ -363,7 +370,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   const int H = a.num_heads;
   const int64_t unit0 = (int64_t)b * a.max_splits * H + h;  // partial of split j: unit0 + j H
   const int d = threadIdx.x;
-  const float* po = a.part_o + unit0 * D + d;
+  const float* po = a.part_o + unit0 * D + partial_slot(d);
   const int64_t stride = (int64_t)H * D;
   if (nsplit <= kCombineFast) {
     // Every load of the merge is issued at once: lane j < nsplit of each wavefront reads
