@@ -155,6 +155,39 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride,
                            int32_t cached_prefix_keys, pk_stream_t stream);
 
 /*
+ * pk_qkv_decode_attention -- one decode step of an attention layer from the fused qkv
+ * projection, in one split-K launch (no counterpart in the reference: it is
+ * pk_qk_norm_rope_store(qkv, ..., k_cache, v_cache, slot_mapping) followed by
+ * pk_varlen_attention_ex(q, ..., k_cache, v_cache, block_table, ...) for a batch in which
+ * every sequence has one query row, i.e. src/models/qwen3.py:80-89 plus
+ * src/layers/attention.py:87-104 on a decode step). Results are bit-identical to those
+ * two calls. qkv is (num_seqs, (num_heads + 2 num_kv_heads) head_dim) with row stride
+ * qkv_row_stride; positions (num_seqs,) int64; cos_sin, norm weights, eps and num_slots as
+ * for pk_qk_norm_rope_store; caches, block table, lengths and workspace as for
+ * pk_varlen_attention_ex with max_seqlen_q = 1 (workspace: pk_varlen_attention_workspace_bytes
+ * with max_seqlen_q = 1). cu_seqlens_q must give every sequence one row (graph padding
+ * rows: 0 or fewer keys and slot -1). slot_mapping[i] must be the cache slot of the last
+ * key of sequence i (the token's own position), as the runner builds it: the key is
+ * written there and read back through the block table by the same wavefront.
+ */
+int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride,
+                            const int64_t* positions, const float* cos_sin, int64_t max_position,
+                            const void* q_norm_weight, const void* k_norm_weight, float eps,
+                            void* k_cache, void* v_cache,
+                            int64_t k_row_stride, int64_t v_row_stride,
+                            int64_t k_block_stride, int64_t v_block_stride,
+                            const int32_t* slot_mapping, int64_t num_slots,
+                            const int32_t* block_table, int32_t block_table_stride,
+                            int32_t block_size,
+                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                            int32_t num_seqs, int32_t max_seqlen_k,
+                            int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                            float softmax_scale,
+                            void* out, int64_t out_row_stride,
+                            void* workspace, size_t workspace_bytes,
+                            int32_t cached_prefix_keys, pk_stream_t stream);
+
+/*
  * Bytes of workspace pk_varlen_attention needs for these launch bounds: the
  * split-K partial outputs of the decode kernel (none when every sequence fits
  * one split) and, when max_seqlen_q > 1, the prefill work plan (work list,

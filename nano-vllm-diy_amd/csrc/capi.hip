@@ -115,7 +115,7 @@ int check_linear(const char* what, const void* x, int64_t x_row_stride, const vo
 
 extern "C" {
 
-int pk_abi_version(void) { return 5; }
+int pk_abi_version(void) { return 6; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -190,16 +190,32 @@ int pk_varlen_attention(const void* q, int64_t q_row_stride, const void* k, cons
                                 workspace_bytes, PK_CACHED_PREFIX_KEYS_DEFAULT, stream);
 }
 
-int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, const void* v,
-                           int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
-                           int64_t v_block_stride, const int32_t* block_table,
-                           int32_t block_table_stride, int32_t block_size,
-                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
-                           int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
-                           int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
-                           int32_t causal, void* out, int64_t out_row_stride, void* workspace,
-                           size_t workspace_bytes, int32_t cached_prefix_keys, pk_stream_t stream) {
-  g_last_error.clear();
+namespace {
+
+// Inputs of the fused decode step's producer (pk_qkv_decode_attention).
+struct FusedProducer {
+  const void* qkv;
+  int64_t qkv_row_stride;
+  const int64_t* positions;
+  const float* cos_sin;
+  int64_t max_position;
+  const void* q_norm;
+  const void* k_norm;
+  float eps;
+  const int32_t* slot_mapping;
+  int64_t num_slots;
+};
+
+// Shared body of pk_varlen_attention_ex and pk_qkv_decode_attention (fp != nullptr: q comes
+// from the fused producer, q itself is unused).
+int attention_impl(const void* q, int64_t q_row_stride, const void* k, const void* v, int64_t k_row_stride,
+                   int64_t v_row_stride, int64_t k_block_stride, int64_t v_block_stride,
+                   const int32_t* block_table, int32_t block_table_stride, int32_t block_size,
+                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                   int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
+                   int32_t head_dim, float softmax_scale, int32_t causal, void* out, int64_t out_row_stride,
+                   void* workspace, size_t workspace_bytes, int32_t cached_prefix_keys, const FusedProducer* fp,
+                   pk_stream_t stream) {
   if (head_dim != pk::kHeadDim)
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: head_dim=%d not built (only %d)", head_dim, pk::kHeadDim);
   if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
@@ -212,7 +228,7 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, c
   if (group != 1 && group != 2 && group != 4 && group != 8)
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: GQA group %d not built (1, 2, 4, 8)", group);
   if (num_seqs == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) return PK_OK;
-  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k)
+  if ((!q && !fp) || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k)
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: null pointer argument");
   // the prefill work list packs key-tile indices in 16 bits and the kv head in 8
   if (max_seqlen_k > kMaxSeqlen || max_seqlen_q > kMaxSeqlen)
@@ -222,6 +238,7 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, c
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: num_kv_heads=%d above 255", num_kv_heads);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: q/k/v/out must be 16-byte aligned");
+  if (fp) q_row_stride = (int64_t)num_heads * head_dim;  // unused: q comes from qkv
   const int64_t kv_row = (int64_t)num_kv_heads * head_dim;
   if (q_row_stride < (int64_t)num_heads * head_dim || out_row_stride < (int64_t)num_heads * head_dim ||
       k_row_stride < kv_row || v_row_stride < kv_row)
@@ -282,6 +299,18 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, c
   a.out = static_cast<uint16_t*>(out);
   a.out_row_stride = out_row_stride;
   a.stream_from = cached_prefix_keys;
+  if (fp) {
+    a.qkv = static_cast<const uint16_t*>(fp->qkv);
+    a.qkv_row_stride = fp->qkv_row_stride;
+    a.positions = fp->positions;
+    a.cos_sin = fp->cos_sin;
+    a.max_position = fp->max_position;
+    a.q_norm = static_cast<const uint16_t*>(fp->q_norm);
+    a.k_norm = static_cast<const uint16_t*>(fp->k_norm);
+    a.norm_eps = fp->eps;
+    a.slot_mapping = fp->slot_mapping;
+    a.num_slots = fp->num_slots;
+  }
   a.split_tokens = ws.split_tokens;
   a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
   char* const wsb = static_cast<char*>(workspace);
@@ -306,6 +335,57 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, c
   if (max_seqlen_q > 1)
     rc = hip_status(pk::launch_prefill(a, group, paged, causal != 0, max_seqlen_q, s), "prefill launch");
   return rc;
+}
+
+}  // namespace
+
+int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, const void* v,
+                           int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                           int64_t v_block_stride, const int32_t* block_table,
+                           int32_t block_table_stride, int32_t block_size,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                           int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+                           int32_t causal, void* out, int64_t out_row_stride, void* workspace,
+                           size_t workspace_bytes, int32_t cached_prefix_keys, pk_stream_t stream) {
+  g_last_error.clear();
+  return attention_impl(q, q_row_stride, k, v, k_row_stride, v_row_stride, k_block_stride, v_block_stride,
+                        block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs,
+                        max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, causal, out,
+                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, nullptr, stream);
+}
+
+int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,
+                            const float* cos_sin, int64_t max_position, const void* q_norm_weight,
+                            const void* k_norm_weight, float eps, void* k_cache, void* v_cache,
+                            int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                            int64_t v_block_stride, const int32_t* slot_mapping, int64_t num_slots,
+                            const int32_t* block_table, int32_t block_table_stride, int32_t block_size,
+                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                            int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                            float softmax_scale, void* out, int64_t out_row_stride, void* workspace,
+                            size_t workspace_bytes, int32_t cached_prefix_keys, pk_stream_t stream) {
+  g_last_error.clear();
+  if (num_seqs <= 0 || max_seqlen_k <= 0) return num_seqs < 0 || max_seqlen_k < 0 ?
+      fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: negative num_seqs / max_seqlen_k") : PK_OK;
+  if (!qkv || !positions || !cos_sin || !slot_mapping || !block_table)
+    return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: null qkv / positions / cos_sin / slot_mapping / block_table");
+  if (max_position <= 0) return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: max_position must be positive");
+  if (!(eps >= 0.f)) return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: eps must be >= 0");
+  if (num_slots < 0) return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: num_slots < 0");
+  const int64_t row = (int64_t)(num_heads + 2 * num_kv_heads) * head_dim;
+  if (qkv_row_stride < row || qkv_row_stride % 8 != 0)
+    return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: qkv_row_stride=%lld must be >= %lld and a multiple of 8",
+                (long long)qkv_row_stride, (long long)row);
+  if (!aligned16(qkv) || !aligned16(cos_sin) || (q_norm_weight && !aligned16(q_norm_weight)) ||
+      (k_norm_weight && !aligned16(k_norm_weight)))
+    return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: qkv / cos_sin / norm weights must be 16-byte aligned");
+  const FusedProducer fp{qkv, qkv_row_stride, positions, cos_sin, max_position, q_norm_weight, k_norm_weight,
+                         eps, slot_mapping, num_slots};
+  return attention_impl(nullptr, 0, k_cache, v_cache, k_row_stride, v_row_stride, k_block_stride, v_block_stride,
+                        block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs, 1,
+                        max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, 1, out, out_row_stride,
+                        workspace, workspace_bytes, cached_prefix_keys, &fp, stream);
 }
 
 int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,

@@ -60,6 +60,19 @@ struct AttnArgs {
   int32_t pf_part_cap;
   int32_t pf_slots;             // persistent work-groups of the prefill kernel
   int32_t prefill_qtiles;       // upper bound on query tiles per sequence (from max_seqlen_q)
+  // Fused decode step (qkv != nullptr): q is the per-head RMSNorm + RoPE of the q part of
+  // the fused qkv row of the sequence's token, and the split holding the sequence's last key
+  // first stores that token's normalised + rotated K row and raw V row at slot_mapping.
+  const uint16_t* qkv;
+  int64_t qkv_row_stride;
+  const int64_t* positions;
+  const float* cos_sin;         // (max_position, D): cos in [0, D/2), sin in [D/2, D)
+  int64_t max_position;
+  const uint16_t* q_norm;       // (D,) bf16 or nullptr
+  const uint16_t* k_norm;
+  float norm_eps;
+  const int32_t* slot_mapping;
+  int64_t num_slots;            // > 0: slots outside [0, num_slots) are not written
 };
 
 // Prefill plan sizes. The kernel runs kPrefillSlotsMax persistent work-groups at most (one

@@ -22,7 +22,7 @@
 //   * softmax: keys of a step are lane-local, so the running max needs no shuffles.
 //   * P.V: p rounded to bf16 and paired across two keys, one dot2 per (head, element).
 // Loads are software-pipelined two steps deep and all issued before the step's math.
-#include "common.h"
+#include "norm_rope.h"
 
 namespace pk {
 namespace {
@@ -117,14 +117,25 @@ struct DecodeState {
 // in-flight loads: the write-after-write wait then drained the pipeline every other step.)
 // STREAM selects non-temporal loads; it is a template parameter (not a runtime branch)
 // so the pipelined loop stays straight-line and its wait counts stay exact.
-template <int U, bool PAGED, bool STREAM>
+// Block id of entry j of a (wave-uniform) block-table row, as a scalar load. The fused
+// decode step stores K/V rows before its loop, after which the compiler can no longer prove
+// the table unchanged: a plain load would become a vector load whose value the compiler
+// treats as divergent, and every buffer load built on it would run in a waterfall loop.
+__device__ __forceinline__ int scalar_block_id(const int32_t* row, int j) {
+  int v;
+  asm volatile("s_load_dword %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(row), "s"(j * 4));
+  return v;
+}
+
+template <int U, bool PAGED, bool STREAM, bool FUSED>
 __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_bytes, int b, int k0, int t,
                                             int t_end, u32x4 (&kr)[U], u32x4 (&vr)[U]) {
   const uint16_t* kp;
   const uint16_t* vp;
   if constexpr (PAGED) {
     // [t, t + U) lies inside one cache block: U divides block_size and split_tokens.
-    const int blk = a.block_table[(int64_t)b * a.bt_stride + t / a.block_size];
+    const int blk = FUSED ? scalar_block_id(a.block_table + (int64_t)b * a.bt_stride, t / a.block_size)
+                          : a.block_table[(int64_t)b * a.bt_stride + t / a.block_size];
     const int off = t % a.block_size;
     kp = a.k + (int64_t)blk * a.k_block_stride + (int64_t)off * a.k_row_stride;
     vp = a.v + (int64_t)blk * a.v_block_stride + (int64_t)off * a.v_row_stride;
@@ -150,7 +161,7 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_byt
 // and the wait counts stay exact. The scheduling barriers keep each step's loads together
 // ahead of its math: otherwise the scheduler sinks every load next to its first use to
 // save registers, which serialises their latency.
-template <int G, int U, bool PAGED, bool STREAM>
+template <int G, int U, bool PAGED, bool STREAM, bool FUSED>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
                                              int k0, int t_begin, int t_end);
 
@@ -220,26 +231,75 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
   }
 }
 
-template <int G, int U, bool PAGED, bool STREAM>
+template <int G, int U, bool PAGED, bool STREAM, bool FUSED>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
                                              int k0, int t_begin, int t_end) {
   const float c2 = a.scale_log2;
   u32x4 kA[U], vA[U], kB[U], vB[U];
-  issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
+  issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
   for (int t = t_begin; t < t_end; t += 2 * U) {
     const int t1 = t + U;
-    issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
+    issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
     __builtin_amdgcn_sched_barrier(0);
     consume<G, U>(st, c2, t, t_end, kA, vA);
     if (t1 >= t_end) break;
     const int t2 = t1 + U;
-    issue_loads<U, PAGED, STREAM>(a, lane_bytes, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
+    issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
     __builtin_amdgcn_sched_barrier(0);
     consume<G, U>(st, c2, t1, t_end, kB, vB);
   }
 }
 
-template <int G, int U, bool PAGED>
+// Fused decode step: q of this DPP row's kv head g (its G query heads) is the RMSNorm +
+// RoPE of the token's fused qkv row, computed here exactly as the producer kernel computes
+// it (norm_rope.h). The split holding the sequence's last key -- the token itself, which
+// attends to its own key (attention.py:87-88 stores before attending) -- first writes the
+// token's normalised + rotated K row and raw V row of kv head g into the cache slot, and
+// waits for those stores before any K/V load: the same wavefront reads that row back in
+// its last pipeline step, and no other work-group reads it. The slot must be the cache
+// position of the sequence's last key (as the runner builds slot_mapping, model_runner.py:
+// 200-210).
+template <int G>
+__device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>& st, int q0, int g, int c,
+                                               bool row_live, bool stores_token) {
+  constexpr int D = kHeadDim;
+  const bool lower = c < kLanesPerRow / 2;
+  float cv[8], sv[8];
+  rope_cos_sin_row(a.cos_sin, a.max_position, a.positions[q0], c, cv, sv);
+  const uint16_t* row = a.qkv + (int64_t)q0 * a.qkv_row_stride + c * 8;
+  uint4 w[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) w[i] = *reinterpret_cast<const uint4*>(row + (g * G + i) * D);
+  int32_t slot = -1;
+  uint4 wk, wv;
+  if (stores_token) {
+    slot = a.slot_mapping[q0];
+    if (slot < 0 || (a.num_slots > 0 && (int64_t)slot >= a.num_slots)) slot = -1;
+    wk = *reinterpret_cast<const uint4*>(row + (a.num_heads + g) * D);
+    wv = *reinterpret_cast<const uint4*>(row + (a.num_heads + a.num_kv_heads + g) * D);
+  }
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const uint4 o = norm_rope_row(w[i], a.q_norm, a.norm_eps, cv, sv, lower, c);
+    st.qp[i][0] = o.x;
+    st.qp[i][1] = o.y;
+    st.qp[i][2] = o.z;
+    st.qp[i][3] = o.w;
+  }
+  if (slot >= 0) {  // uniform over the work-group: one token per sequence
+    const uint4 ok = norm_rope_row(wk, a.k_norm, a.norm_eps, cv, sv, lower, c);
+    if (row_live) {
+      const int64_t blk = slot / a.block_size, off = slot - blk * a.block_size;
+      uint16_t* kd = const_cast<uint16_t*>(a.k) + blk * a.k_block_stride + off * a.k_row_stride + g * D + c * 8;
+      uint16_t* vd = const_cast<uint16_t*>(a.v) + blk * a.v_block_stride + off * a.v_row_stride + g * D + c * 8;
+      *reinterpret_cast<uint4*>(kd) = ok;
+      *reinterpret_cast<uint4*>(vd) = wv;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stores are done; no load moves above
+  }
+}
+
+template <int G, int U, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
   static_assert(U % 2 == 0, "P.V pairs keys");
   constexpr int D = kHeadDim;
@@ -274,13 +334,20 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   // q stays in bf16 pairs: q.k runs on v_dot2_f32_bf16 and the scale is applied to the
   // fp32 dot product (scores are kept unscaled; c2 enters the exponent).
   DecodeState<G> st;
+  if constexpr (FUSED) {
+    fused_producer<G>(a, st, q0, g, c, row_live, t_end == Lk);
+  } else {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + (g * G + i) * D + c * 8);
+      st.qp[i][0] = w.x;
+      st.qp[i][1] = w.y;
+      st.qp[i][2] = w.z;
+      st.qp[i][3] = w.w;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + (g * G + i) * D + c * 8);
-    st.qp[i][0] = w.x;
-    st.qp[i][1] = w.y;
-    st.qp[i][2] = w.z;
-    st.qp[i][3] = w.w;
     st.m[i] = -INFINITY;
     st.l[i] = 0.f;
 #pragma unroll
@@ -293,9 +360,9 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   // once per step and only displaces useful lines. Decided per split (by its first key).
   const bool stream = a.stream_from >= 0 && t_begin >= a.stream_from;
   if (stream)
-    decode_range<G, U, PAGED, true>(st, a, lane_bytes, b, k0, t_begin, t_end);
+    decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end);
   else
-    decode_range<G, U, PAGED, false>(st, a, lane_bytes, b, k0, t_begin, t_end);
+    decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end);
 
   if (!row_live) return;
   // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous,
@@ -430,10 +497,12 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const int zgroups = quads / waves;
   const dim3 grid((unsigned)(a.max_splits * a.num_seqs), (unsigned)zgroups);
   const dim3 block((unsigned)(waves * kWave));
-  if (paged)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true>), grid, block, 0, stream, a);
+  if (a.qkv != nullptr)  // the fused decode step is paged only (checked by its entry point)
+    hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);
+  else if (paged)
+    hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<G, U, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

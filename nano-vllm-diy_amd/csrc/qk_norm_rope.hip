@@ -20,40 +20,12 @@
 // lane c ^ 8, one DPP row rotation by 8 away. The sum of squares of the norm is a 16-lane
 // DPP reduction. In the fused row [q heads | k heads | v heads] head row r starts at
 // element r * D, so every row is addressed the same way.
-#include "common.h"
+#include "norm_rope.h"
 
 namespace pk {
 namespace {
 
 constexpr int kProdThreads = 256;
-constexpr int kLanesPerRow = kHeadDim / 8;   // 16: one DPP row per head row
-constexpr int kDppRowRor8 = 0x128;           // row_ror:8 -> lane (c + 8) mod 16 = c ^ 8
-
-__device__ __forceinline__ float dpp_ror8(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kDppRowRor8, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float round_bf16(float f) {
-  return __uint_as_float((uint32_t)f32_to_bf16(f) << 16);
-}
-
-__device__ __forceinline__ void unpack8(const uint4 w, float f[8]) {
-  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
-  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
-  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
-  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
-}
-
-__device__ __forceinline__ uint4 pack8(const float f[8]) {
-  uint4 w;
-  w.x = pack_bf16x2(f[0], f[1]);
-  w.y = pack_bf16x2(f[2], f[3]);
-  w.z = pack_bf16x2(f[4], f[5]);
-  w.w = pack_bf16x2(f[6], f[7]);
-  return w;
-}
-
 struct ProducerArgs {
   const uint16_t* qkv;          // (N, (Hq + 2 Hkv) * D), row stride qkv_row_stride
   int64_t qkv_row_stride;
@@ -86,38 +58,6 @@ constexpr int kRowsInFlight = PK_PROD_ROWS_IN_FLIGHT;
 #define PK_PROD_SPREAD_BELOW 1024
 #endif
 
-// Normalise + rotate one head row held as 8 elements per lane; returns the packed bf16 row.
-__device__ __forceinline__ uint4 norm_rope_row(const uint4 w, const uint16_t* wt, float eps,
-                                               const float cv[8], const float sv[8], bool lower,
-                                               int c) {
-  constexpr int D = kHeadDim;
-  float f[8];
-  unpack8(w, f);
-  // RMSNorm (layernorm.py:11-16): fp32, weight multiply, round to bf16.
-  if (wt != nullptr) {
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
-    ss = row16_sum(ss);
-    const float rs = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + eps);
-    float wf[8];
-    unpack8(*reinterpret_cast<const uint4*>(wt + c * 8), wf);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = round_bf16(wf[e] * (f[e] * rs));
-  }
-  // RoPE (pos_embedding.py:37-46): t1 = x[:64], t2 = x[64:];
-  //   out[:64] = t1 cos - t2 sin, out[64:] = t1 sin + t2 cos, cos/sin of column d mod 64.
-  float o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float p = dpp_ror8(f[e]);                  // element d +- 64
-    const float t1 = lower ? f[e] : p;
-    const float t2 = lower ? p : f[e];
-    o[e] = lower ? t1 * cv[e] - t2 * sv[e] : t1 * sv[e] + t2 * cv[e];
-  }
-  return pack8(o);
-}
-
 // One work item = one token's share `part` of `parts` (grid-stride, one wavefront per
 // item): the token's position and slot are wave-uniform loads, the cos/sin row is read once
 // per lane, and DPP row j of the wave walks head rows r = 4 (part + parts i) + j with up to
@@ -139,20 +79,13 @@ __global__ __launch_bounds__(kProdThreads) void qk_norm_rope_store_kernel(const 
     const int32_t token = (int32_t)(item / parts);
     const int part = (int)(item - (int64_t)token * parts);
     const uint16_t* src = a.qkv + (int64_t)token * a.qkv_row_stride + c * 8;
-    int64_t pos = a.positions[token];
-    pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
     int32_t slot = -1;
     if (a.k_cache != nullptr) {
       slot = a.slot_mapping[token];
       if (slot < 0 || (a.num_slots > 0 && (int64_t)slot >= a.num_slots)) slot = -1;
     }
-    const float* cs = a.cos_sin + pos * D + (c & 7) * 8;
-    const float4 c0 = *reinterpret_cast<const float4*>(cs);
-    const float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
-    const float4 s0 = *reinterpret_cast<const float4*>(cs + D / 2);
-    const float4 s1 = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
-    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float cv[8], sv[8];
+    rope_cos_sin_row(a.cos_sin, a.max_position, a.positions[token], c, cv, sv);
 
     const int stride = 4 * parts;                                // between this row's head rows
     for (int base = 4 * part + row0; base < rows; base += stride * kRowsInFlight) {

@@ -14,6 +14,9 @@ import torch
 
 from ._lib import check, lib
 
+# pk_varlen_attention's cache hint (include/pagedkv.h): keys below it are read with normal loads
+PK_CACHED_PREFIX_KEYS_DEFAULT = 2048
+
 _workspaces: dict[int, torch.Tensor] = {}  # device index -> workspace of graph-captured calls
 
 
@@ -207,6 +210,80 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         check(lib().pk_varlen_attention(*args, _stream(q)), "pk_varlen_attention")
     else:
         check(lib().pk_varlen_attention_ex(*args, int(cached_prefix_keys), _stream(q)), "pk_varlen_attention_ex")
+    return out
+
+
+def qkv_decode_attention(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: torch.Tensor,
+                         num_heads: int, num_kv_heads: int, head_dim: int,
+                         q_norm_weight: torch.Tensor | None, k_norm_weight: torch.Tensor | None, eps: float,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                         cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_k: int,
+                         softmax_scale: float | None, block_table: torch.Tensor,
+                         out: torch.Tensor | None = None, cached_prefix_keys: int | None = None,
+                         check_slots: bool = False, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode step of an attention layer from the fused qkv projection: q/k RMSNorm +
+    RoPE, the new K/V rows stored at slot_mapping and paged decode attention, in one launch.
+    Bit-identical to qk_norm_rope_store(qkv, ..., k_cache, v_cache, slot_mapping) followed by
+    varlen_attention(q, k_cache, v_cache, ..., max_seqlen_q=1, block_table=...)
+    (src/models/qwen3.py:80-89 and src/layers/attention.py:87-104 on a decode step). Every
+    sequence has one query row (cu_seqlens_q = arange, graph padding rows aside) and
+    slot_mapping[i] is the cache slot of sequence i's last key. Returns out (S, Hq, D) bf16.
+    """
+    if qkv.dim() != 2 or qkv.dtype != torch.bfloat16 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be (S, (Hq + 2 Hkv) * D) bf16 with contiguous rows")
+    n = qkv.shape[0]
+    dev = qkv.device
+    if qkv.shape[1] != (num_heads + 2 * num_kv_heads) * head_dim:
+        raise ValueError(f"qkv width {qkv.shape[1]} != (Hq + 2 Hkv) * D")
+    if positions.dtype != torch.int64 or positions.device != dev or positions.numel() != n or \
+            not positions.is_contiguous():
+        raise ValueError("positions must be a contiguous (S,) int64 tensor on the qkv device")
+    if cos_sin.dim() == 3:
+        cos_sin = cos_sin.squeeze(1)
+    if cos_sin.dtype != torch.float32 or cos_sin.shape[-1] != head_dim or \
+            not cos_sin.is_contiguous() or cos_sin.device != dev:
+        raise ValueError("cos_sin must be a contiguous (P, D) float32 table on the qkv device")
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w is not None and (w.dtype != torch.bfloat16 or w.numel() != head_dim or
+                              not w.is_contiguous() or w.device != dev):
+            raise ValueError(f"{name} must be a contiguous ({head_dim},) bf16 tensor on the qkv device")
+    _req_i32("slot_mapping", slot_mapping, dev)
+    _req_i32("cu_seqlens_q", cu_seqlens_q, dev)
+    _req_i32("cu_seqlens_k", cu_seqlens_k, dev)
+    _req_i32("block_table", block_table, dev)
+    num_seqs = cu_seqlens_q.numel() - 1
+    if slot_mapping.numel() != n or not slot_mapping.is_contiguous() or num_seqs != n or \
+            cu_seqlens_k.numel() != n + 1 or not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):
+        raise ValueError("a decode step has one qkv row, one slot and one (q, k) length pair per sequence")
+    if block_table.dim() != 2 or block_table.stride(1) != 1 or block_table.shape[0] < num_seqs:
+        raise ValueError("block_table must be (S, W) with contiguous rows")
+    row = num_kv_heads * head_dim
+    for c in (k_cache, v_cache):
+        if c.dim() != 4 or c.dtype != torch.bfloat16 or c.device != dev or c.stride(-1) != 1 or \
+                c.stride(-2) != head_dim or c.shape[-2] != num_kv_heads or c.shape[-1] != head_dim:
+            raise ValueError("caches must be (NB, BS, Hkv, D) bf16 with contiguous heads")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache shapes differ")
+    num_slots = k_cache.shape[0] * k_cache.shape[1] if check_slots else 0
+    if out is None:
+        out = torch.empty(n, num_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    elif out.shape != (n, num_heads, head_dim) or out.dtype != torch.bfloat16 or out.stride(-1) != 1 or \
+            out.stride(1) != head_dim:
+        raise ValueError("out must be (S, Hq, D) bf16 with contiguous heads")
+    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    nbytes = workspace_bytes(num_seqs, num_heads, head_dim, 1, max_seqlen_k)
+    ws = _workspace(nbytes, dev) if workspace is None else _given_workspace(workspace, nbytes, dev)
+    hint = PK_CACHED_PREFIX_KEYS_DEFAULT if cached_prefix_keys is None else int(cached_prefix_keys)
+    ptr = lambda t: t.data_ptr() if t is not None else 0  # noqa: E731
+    check(lib().pk_qkv_decode_attention(
+        qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
+        ptr(q_norm_weight), ptr(k_norm_weight), float(eps), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.stride(1), v_cache.stride(1), k_cache.stride(0), v_cache.stride(0),
+        slot_mapping.data_ptr(), num_slots, block_table.data_ptr(), block_table.stride(0), k_cache.shape[1],
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_k),
+        num_heads, num_kv_heads, head_dim, scale, out.data_ptr(), out.stride(0),
+        ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0, hint, _stream(qkv)),
+        "pk_qkv_decode_attention")
     return out
 
 

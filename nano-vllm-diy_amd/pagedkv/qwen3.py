@@ -100,6 +100,9 @@ class Qwen3Model:
         eps = cfg.rms_norm_eps
         flat = ctx.block_tables is None
         small = input_ids.shape[0] <= ops.LINEAR_MAX_ROWS
+        # a decode step: every sequence has one new token (cu_seqlens_q = arange), read
+        # through block tables; the producer then runs inside the attention launch
+        decode = not flat and ctx.max_seqlen_q == 1 and input_ids.shape[0] == ctx.cu_seqlens_q.numel() - 1
         h = F.embedding(input_ids, W.embed)
         residual = None
         nl = len(W.layers)
@@ -111,18 +114,23 @@ class Qwen3Model:
                 x, residual = ops.add_rmsnorm(h, L["input_norm"], eps, residual=residual)
             qkv = ops.linear(x, L["qkv"]) if small else F.linear(x, L["qkv"])
             kc, vc = self.k_caches[li], self.v_caches[li]
-            q, k = ops.qk_norm_rope_store(qkv, positions, self.cos_sin, Hq, Hkv, D, L["q_norm"],
-                                          L["k_norm"], eps, kc, vc, ctx.slot_mapping, return_k=flat)
-            if flat:
-                v = qkv[:, (Hq + Hkv) * D:].view(-1, Hkv, D)
-                o = ops.varlen_attention(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
-                                         ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True)
+            if decode:
+                # one launch: q/k norm + RoPE, the K/V store and paged decode attention; no
+                # block is shared (no prefix cache), so every decode read streams
+                o = ops.qkv_decode_attention(qkv, positions, self.cos_sin, Hq, Hkv, D, L["q_norm"], L["k_norm"],
+                                             eps, kc, vc, ctx.slot_mapping, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                             ctx.max_seqlen_k, self.scale, ctx.block_tables, cached_prefix_keys=0)
             else:
-                # this engine has no prefix cache: no block is shared between sequences, so
-                # every decode read streams (cached_prefix_keys=0)
-                o = ops.varlen_attention(q, kc, vc, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
-                                         ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True,
-                                         ctx.block_tables, cached_prefix_keys=0)
+                q, k = ops.qk_norm_rope_store(qkv, positions, self.cos_sin, Hq, Hkv, D, L["q_norm"],
+                                              L["k_norm"], eps, kc, vc, ctx.slot_mapping, return_k=flat)
+                if flat:
+                    v = qkv[:, (Hq + Hkv) * D:].view(-1, Hkv, D)
+                    o = ops.varlen_attention(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                             ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True)
+                else:
+                    o = ops.varlen_attention(q, kc, vc, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                             ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale, True,
+                                             ctx.block_tables, cached_prefix_keys=0)
             if small:
                 x, residual = ops.linear_add_rmsnorm(o.view(-1, Hq * D), L["o"], residual,
                                                      L["post_norm"], eps, residual_out=residual)

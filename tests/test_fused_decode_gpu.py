@@ -1,0 +1,122 @@
+"""GPU parity of the fused decode step (pk_qkv_decode_attention, through the C-ABI) against
+its unfused form, pk_qk_norm_rope_store followed by pk_varlen_attention_ex over the block
+tables: the attention output and both caches must be bit-identical, for GQA groups 1, 2, 4,
+sequences of one to several splits (the last split stores the token's K/V row and reads it
+back), and graph-style padding rows (zero-length sequences, slot -1) that must leave the
+caches untouched. The unfused path is itself pinned against the oracle by
+test_producer_gpu.py and test_kernels_gpu.py.
+"""
+import math
+
+import pytest
+import torch
+
+import pagedkv
+from pagedkv import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+BS = 256
+EPS = 1e-6
+MAX_POS = 40960
+
+
+def _batch(lens, hq, hkv, seed, dev, pad=0):
+    g = torch.Generator().manual_seed(seed)
+    S = len(lens)
+    nb = sum(math.ceil(lk / BS) for lk in lens) + 2
+    tables = W._pop_tables(lens, torch.randperm(nb, generator=g).tolist())
+    width = max(len(t) for t in tables)
+    bt = torch.full((S + pad, width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    kc = torch.randn(nb, BS, hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, BS, hkv, D, generator=g).to(torch.bfloat16)
+    qkv = (torch.randn(S + pad, (hq + 2 * hkv) * D, generator=g) * 3).to(torch.bfloat16)
+    pos = torch.tensor([lk - 1 for lk in lens] + [0] * pad, dtype=torch.int64)
+    slot = torch.tensor([tables[i][(lk - 1) // BS] * BS + (lk - 1) % BS for i, lk in enumerate(lens)] +
+                        [-1] * pad, dtype=torch.int32)
+    # graph padding as the reference runner writes it: cumulative lengths, then a zero tail
+    cu_q = torch.tensor(list(range(S + 1)) + [0] * pad, dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()) + [0] * pad, dtype=torch.int32)
+    qw = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    to = lambda t: t.to(dev)  # noqa: E731
+    return dict(qkv=to(qkv), pos=to(pos), slot=to(slot), cu_q=to(cu_q), cu_k=to(cu_k), bt=to(bt), kc=to(kc),
+                vc=to(vc), qw=to(qw), kw=to(kw), maxk=max(lens), S=S)
+
+
+def _both(b, hq, hkv, cs, hint=0):
+    scale = D ** -0.5
+    kca, vca = b["kc"].clone(), b["vc"].clone()
+    q, _ = pagedkv.qk_norm_rope_store(b["qkv"], b["pos"], cs, hq, hkv, D, b["qw"], b["kw"], EPS, kca, vca,
+                                      b["slot"])
+    out_a = pagedkv.varlen_attention(q, kca, vca, b["cu_q"], b["cu_k"], 1, b["maxk"], scale, True, b["bt"],
+                                     cached_prefix_keys=hint)
+    kcb, vcb = b["kc"].clone(), b["vc"].clone()
+    out_b = pagedkv.qkv_decode_attention(b["qkv"], b["pos"], cs, hq, hkv, D, b["qw"], b["kw"], EPS, kcb, vcb,
+                                         b["slot"], b["cu_q"], b["cu_k"], b["maxk"], scale, b["bt"],
+                                         cached_prefix_keys=hint)
+    torch.cuda.synchronize()
+    return (out_a, kca, vca), (out_b, kcb, vcb)
+
+
+def _assert_same(a, b, S):
+    out_a, kca, vca = a
+    out_b, kcb, vcb = b
+    assert torch.equal(out_a[:S].view(torch.int16), out_b[:S].view(torch.int16)), "attention output differs"
+    assert torch.equal(kca.view(torch.int16), kcb.view(torch.int16)), "K cache differs"
+    assert torch.equal(vca.view(torch.int16), vcb.view(torch.int16)), "V cache differs"
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4)])
+@pytest.mark.parametrize("lens,pad", [([1, 5, 255, 256, 257, 3000], 0), ([700, 12, 4096, 1], 3)])
+def test_fused_decode_bit_identical_to_producer_then_attention(gpu, hq, hkv, lens, pad):
+    cs = pagedkv.rope_cos_sin(MAX_POS, D, 1000000.0, gpu)
+    b = _batch(lens, hq, hkv, seed=len(lens) + hq + pad, dev=gpu, pad=pad)
+    a, f = _both(b, hq, hkv, cs)
+    _assert_same(a, f, b["S"])
+
+
+def test_fused_decode_serving_batch_and_cache_hints(gpu):
+    """128 sequences of 100-2048 keys (a serving decode step), every cache hint."""
+    g = torch.Generator().manual_seed(11)
+    lens = W._uniform(g, 100, 2048, 128)
+    cs = pagedkv.rope_cos_sin(MAX_POS, D, 1000000.0, gpu)
+    b = _batch(lens, 16, 8, seed=12, dev=gpu)
+    for hint in (0, -1, 1024):
+        a, f = _both(b, 16, 8, cs, hint=hint)
+        _assert_same(a, f, b["S"])
+
+
+def test_fused_decode_in_graph_replays(gpu):
+    """Captured once, replayed on new qkv rows: every replay equals the eager unfused step."""
+    cs = pagedkv.rope_cos_sin(MAX_POS, D, 1000000.0, gpu)
+    b = _batch([40, 600, 2100, 9, 1300], 16, 8, seed=21, dev=gpu, pad=3)
+    S = b["S"]
+    pagedkv.reserve_workspace(S + 3, 16, 128, 1, b["maxk"], gpu)
+    kcg, vcg = b["kc"].clone(), b["vc"].clone()
+    qkv = b["qkv"].clone()
+    out = torch.empty(S + 3, 16, D, dtype=torch.bfloat16, device=gpu)
+
+    def step():
+        pagedkv.qkv_decode_attention(qkv, b["pos"], cs, 16, 8, D, b["qw"], b["kw"], EPS, kcg, vcg, b["slot"],
+                                     b["cu_q"], b["cu_k"], b["maxk"], D ** -0.5, b["bt"], out=out,
+                                     cached_prefix_keys=0)
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    g = torch.Generator().manual_seed(5)
+    for r in range(3):
+        qkv.copy_((torch.randn(qkv.shape, generator=g) * 3).to(torch.bfloat16).to(gpu))
+        graph.replay()
+        torch.cuda.synchronize()
+        b2 = dict(b, qkv=qkv.clone(), kc=kcg.clone(), vc=vcg.clone())
+        # the replay already stored this step's rows: the unfused step on the same inputs
+        # stores the same rows again and must produce the same output
+        a, _ = _both(b2, 16, 8, cs)
+        assert torch.equal(a[0][:S].view(torch.int16), out[:S].view(torch.int16)), f"replay {r}"
+        assert torch.equal(a[1].view(torch.int16), kcg.view(torch.int16)), f"replay {r}: K cache"
