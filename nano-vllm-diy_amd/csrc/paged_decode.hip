@@ -314,12 +314,14 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   // every sequence: split 0 always exists, split 15 only for the longest contexts).
   const int split = blockIdx.x / a.num_seqs;
   const int b = (blockIdx.x - split * a.num_seqs + split) % a.num_seqs;
-  const int q0 = a.cu_q[b];
-  if (a.cu_q[b + 1] - q0 != 1) return;  // rows with Lq != 1 belong to the prefill kernel
-  const int k0 = a.cu_k[b];
-  const int Lk = min(a.cu_k[b + 1] - k0, a.max_seqlen_k);
+  // Both length pairs are read before the first branch, in one round of scalar loads: the
+  // two early exits are one test, so neither pair waits behind the other's branch.
+  const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
+  const int k0 = a.cu_k[b], k1 = a.cu_k[b + 1];
+  const int Lk = min(k1 - k0, a.max_seqlen_k);
   const int t_begin = split * a.split_tokens;
-  if (t_begin >= Lk) return;            // also skips Lk <= 0 (graph padding)
+  // rows with Lq != 1 belong to the prefill kernel; t_begin >= Lk also skips Lk <= 0 (graph padding)
+  if ((q1 - q0 != 1) | (t_begin >= Lk)) return;
   const int t_end = min(Lk, t_begin + a.split_tokens);
   const int nsplit = (Lk + a.split_tokens - 1) / a.split_tokens;
 
