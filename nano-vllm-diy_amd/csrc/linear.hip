@@ -275,23 +275,56 @@ __global__ __launch_bounds__(kLinNormThreads) void linear_add_rmsnorm_kernel(
     float eps, uint16_t* out, int64_t out_stride, uint16_t* residual_out, int64_t res_out_stride) {
   const int64_t row = blockIdx.x;
   const int hidden = a.n_out;
+  // The residual and weight rows do not depend on the partial sums: their loads go out
+  // first, and the partials of kNormBatch splits at a time after them, so the kernel waits
+  // for one round of loads per batch instead of one per split plus two more. The splits are
+  // still added in order 0, 1, 2, ... (the fp32 sum is unchanged).
+  constexpr int kNormBatch = 4;
+  uint4 rv[kVecs], wv[kVecs];
+#pragma unroll
+  for (int j = 0; j < kVecs; ++j) {
+    const int col = (j * kLinNormThreads + threadIdx.x) * 8;
+    if (col < hidden) {
+      rv[j] = *reinterpret_cast<const uint4*>(residual + row * res_stride + col);
+      wv[j] = *reinterpret_cast<const uint4*>(weight + col);
+    }
+  }
   float v[kVecs][8];
+#pragma unroll
+  for (int j = 0; j < kVecs; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+  for (int s0 = 0; s0 < a.ks; s0 += kNormBatch) {
+    float4 lo[kNormBatch][kVecs], hi[kNormBatch][kVecs];
+#pragma unroll
+    for (int u = 0; u < kNormBatch; ++u) {
+      const int s = min(s0 + u, a.ks - 1);  // past the last split: re-read it, not added
+#pragma unroll
+      for (int j = 0; j < kVecs; ++j) {
+        const int col = (j * kLinNormThreads + threadIdx.x) * 8;
+        if (col < hidden) {
+          const float* pp = a.part + ((int64_t)s * a.rows + row) * hidden + col;
+          lo[u][j] = *reinterpret_cast<const float4*>(pp);
+          hi[u][j] = *reinterpret_cast<const float4*>(pp + 4);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kNormBatch; ++u) {
+      if (s0 + u >= a.ks) break;
+#pragma unroll
+      for (int j = 0; j < kVecs; ++j) {
+        v[j][0] += lo[u][j].x; v[j][1] += lo[u][j].y; v[j][2] += lo[u][j].z; v[j][3] += lo[u][j].w;
+        v[j][4] += hi[u][j].x; v[j][5] += hi[u][j].y; v[j][6] += hi[u][j].z; v[j][7] += hi[u][j].w;
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kVecs; ++j) {
     const int col = (j * kLinNormThreads + threadIdx.x) * 8;
     if (col < hidden) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
-      for (int s = 0; s < a.ks; ++s) {
-        const float* pp = a.part + ((int64_t)s * a.rows + row) * hidden + col;
-        const float4 lo = *reinterpret_cast<const float4*>(pp);
-        const float4 hi = *reinterpret_cast<const float4*>(pp + 4);
-        v[j][0] += lo.x; v[j][1] += lo.y; v[j][2] += lo.z; v[j][3] += lo.w;
-        v[j][4] += hi.x; v[j][5] += hi.y; v[j][6] += hi.z; v[j][7] += hi.w;
-      }
-      const uint4 rv = *reinterpret_cast<const uint4*>(residual + row * res_stride + col);
-      const uint32_t rr[4] = {rv.x, rv.y, rv.z, rv.w};
+      const uint32_t rr[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         // the linear output is bf16 before the residual add
@@ -315,8 +348,7 @@ __global__ __launch_bounds__(kLinNormThreads) void linear_add_rmsnorm_kernel(
   for (int j = 0; j < kVecs; ++j) {
     const int col = (j * kLinNormThreads + threadIdx.x) * 8;
     if (col < hidden) {
-      const uint4 w = *reinterpret_cast<const uint4*>(weight + col);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
       uint32_t o[4], ro[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

@@ -32,22 +32,32 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     const uint16_t* __restrict__ weight, float eps, int32_t hidden, uint16_t* out, int64_t out_stride,
     uint16_t* residual_out, int64_t res_out_stride) {
   const int64_t row = blockIdx.x;
+  // x, residual and weight loads all go out before any of them is used (one round of loads)
+  uint4 xv[kVecs], rv[kVecs], wv[kVecs];
+#pragma unroll
+  for (int j = 0; j < kVecs; ++j) {
+    const int col = (j * kNormThreads + threadIdx.x) * 8;
+    if (col < hidden) {
+      xv[j] = *reinterpret_cast<const uint4*>(x + row * x_stride + col);
+      rv[j] = residual != nullptr ? *reinterpret_cast<const uint4*>(residual + row * res_stride + col)
+                                  : make_uint4(0, 0, 0, 0);
+      wv[j] = *reinterpret_cast<const uint4*>(weight + col);
+    }
+  }
   float v[kVecs][8];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kVecs; ++j) {
     const int col = (j * kNormThreads + threadIdx.x) * 8;
     if (col < hidden) {
-      const uint4 w = *reinterpret_cast<const uint4*>(x + row * x_stride + col);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t ww[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[j][2 * e] = bf16_lo(ww[e]);
         v[j][2 * e + 1] = bf16_hi(ww[e]);
       }
       if (residual != nullptr) {
-        const uint4 r = *reinterpret_cast<const uint4*>(residual + row * res_stride + col);
-        const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
+        const uint32_t rr[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           v[j][2 * e] += bf16_lo(rr[e]);
@@ -70,8 +80,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
   for (int j = 0; j < kVecs; ++j) {
     const int col = (j * kNormThreads + threadIdx.x) * 8;
     if (col < hidden) {
-      const uint4 w = *reinterpret_cast<const uint4*>(weight + col);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
       uint32_t o[4], ro[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
