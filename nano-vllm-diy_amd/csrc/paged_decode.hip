@@ -161,9 +161,9 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_byt
 // and the wait counts stay exact. The scheduling barriers keep each step's loads together
 // ahead of its math: otherwise the scheduler sinks every load next to its first use to
 // save registers, which serialises their latency.
-template <int G, int U, bool PAGED, bool STREAM, bool FUSED>
+template <int G, int U, bool PAGED, bool STREAM, bool FUSED, class Pre>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
-                                             int k0, int t_begin, int t_end);
+                                             int k0, int t_begin, int t_end, Pre&& pre);
 
 // Fold keys [t, t + U) (already loaded) into the running softmax state.
 template <int G, int U>
@@ -231,12 +231,13 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
   }
 }
 
-template <int G, int U, bool PAGED, bool STREAM, bool FUSED>
+template <int G, int U, bool PAGED, bool STREAM, bool FUSED, class Pre>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
-                                             int k0, int t_begin, int t_end) {
+                                             int k0, int t_begin, int t_end, Pre&& pre) {
   const float c2 = a.scale_log2;
   u32x4 kA[U], vA[U], kB[U], vB[U];
   issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
+  pre();  // q (loaded or computed) while the first K/V loads are in flight
   for (int t = t_begin; t < t_end; t += 2 * U) {
     const int t1 = t + U;
     issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
@@ -334,20 +335,11 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   const uint32_t lane_bytes = (uint32_t)(g * D + c * 8) * 2u;
 
   // q stays in bf16 pairs: q.k runs on v_dot2_f32_bf16 and the scale is applied to the
-  // fp32 dot product (scores are kept unscaled; c2 enters the exponent).
+  // fp32 dot product (scores are kept unscaled; c2 enters the exponent). q is loaded (or,
+  // in the fused decode step, computed) after the first K/V loads are issued, so its
+  // latency overlaps theirs -- except in the fused split that stores the token's K/V row,
+  // which must finish that store before any of its loads.
   DecodeState<G> st;
-  if constexpr (FUSED) {
-    fused_producer<G>(a, st, q0, g, c, row_live, t_end == Lk);
-  } else {
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + (g * G + i) * D + c * 8);
-      st.qp[i][0] = w.x;
-      st.qp[i][1] = w.y;
-      st.qp[i][2] = w.z;
-      st.qp[i][3] = w.w;
-    }
-  }
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     st.m[i] = -INFINITY;
@@ -355,16 +347,38 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
 #pragma unroll
     for (int e = 0; e < 8; ++e) st.acc[i][e] = 0.f;
   }
+  const auto load_q = [&]() {
+    if constexpr (FUSED) {
+      fused_producer<G>(a, st, q0, g, c, row_live, false);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + (g * G + i) * D + c * 8);
+        st.qp[i][0] = w.x;
+        st.qp[i][1] = w.y;
+        st.qp[i][2] = w.z;
+        st.qp[i][3] = w.w;
+      }
+    }
+  };
+  const auto nothing = []() {};
 
   // Keys at positions >= a.stream_from are read with non-temporal (streaming) loads, earlier
   // ones with normal loads: prefix caching can only share a sequence's leading blocks, so
   // those are the reads worth keeping in L2 / Infinity Cache; everything past them is read
   // once per step and only displaces useful lines. Decided per split (by its first key).
   const bool stream = a.stream_from >= 0 && t_begin >= a.stream_from;
-  if (stream)
-    decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end);
-  else
-    decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end);
+  if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
+    fused_producer<G>(a, st, q0, g, c, row_live, true);
+    if (stream)
+      decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, nothing);
+    else
+      decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, nothing);
+  } else if (stream) {
+    decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
+  } else {
+    decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
+  }
 
   if (!row_live) return;
   // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous,
