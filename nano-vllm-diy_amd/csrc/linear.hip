@@ -279,7 +279,7 @@ __global__ __launch_bounds__(kLinNormThreads) void linear_add_rmsnorm_kernel(
   // first, and the partials of kNormBatch splits at a time after them, so the kernel waits
   // for one round of loads per batch instead of one per split plus two more. The splits are
   // still added in order 0, 1, 2, ... (the fp32 sum is unchanged).
-  constexpr int kNormBatch = 4;
+  constexpr int kNormBatch = 8;
   uint4 rv[kVecs], wv[kVecs];
 #pragma unroll
   for (int j = 0; j < kVecs; ++j) {
