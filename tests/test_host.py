@@ -251,3 +251,36 @@ def test_shared_prefix_keys_from_block_reference_counts():
     w4 = make_workload("cfg4")
     assert w4.shared_prefix_keys == 2048 and w4.ctx.cached_prefix_keys == 2048
     assert make_workload("cfg1_decode").shared_prefix_keys == 0
+
+
+def _fused(lib, **kw):
+    fake = ctypes.c_void_p(0x10000)
+    width = (HQ + 2 * HKV) * HEAD_DIM
+    args = dict(qkv=fake, qkv_row_stride=width, positions=fake, cos_sin=fake, max_position=40960,
+                q_norm=fake, k_norm=fake, eps=1e-6, k_cache=fake, v_cache=fake,
+                k_row_stride=HKV * HEAD_DIM, v_row_stride=HKV * HEAD_DIM,
+                k_block_stride=BLOCK_SIZE * HKV * HEAD_DIM, v_block_stride=BLOCK_SIZE * HKV * HEAD_DIM,
+                slot_mapping=fake, num_slots=0, block_table=fake, bt_stride=8, block_size=BLOCK_SIZE,
+                cu_q=fake, cu_k=fake, num_seqs=2, max_k=2048, num_heads=HQ, num_kv_heads=HKV,
+                head_dim=HEAD_DIM, scale=0.088, out=fake, out_row_stride=HQ * HEAD_DIM,
+                ws=None, ws_bytes=0, hint=0, stream=None)
+    args.update(kw)
+    return lib.pk_qkv_decode_attention(*args.values())
+
+
+def test_fused_decode_argument_checks_fail_before_launch():
+    lib = _lib.lib()
+    assert _fused(lib, qkv=None) == _lib.PK_ERR_INVALID_ARG
+    assert b"null" in lib.pk_last_error()
+    assert _fused(lib, block_table=None) == _lib.PK_ERR_INVALID_ARG       # paged only
+    assert _fused(lib, qkv_row_stride=(HQ + 2 * HKV) * HEAD_DIM - 8) == _lib.PK_ERR_INVALID_ARG
+    assert _fused(lib, qkv=ctypes.c_void_p(0x10008)) == _lib.PK_ERR_INVALID_ARG
+    assert b"aligned" in lib.pk_last_error()
+    assert _fused(lib, max_position=0) == _lib.PK_ERR_INVALID_ARG
+    assert _fused(lib, head_dim=64) == _lib.PK_ERR_UNSUPPORTED
+    assert _fused(lib, num_heads=24, qkv_row_stride=(24 + 2 * HKV) * HEAD_DIM) == _lib.PK_ERR_UNSUPPORTED  # GQA 3
+    assert _fused(lib, block_size=100) == _lib.PK_ERR_INVALID_ARG
+    # the split-K partials need a workspace: refused before any launch
+    assert _fused(lib) == _lib.PK_ERR_WORKSPACE
+    assert _fused(lib, num_seqs=-1) == _lib.PK_ERR_INVALID_ARG
+    assert _fused(lib, num_seqs=0) == _lib.PK_OK
