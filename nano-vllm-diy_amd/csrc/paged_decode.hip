@@ -56,7 +56,7 @@ constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through
 // sets stay there, dirty, until the kernel ends; larger ones get evicted in the middle of the
 // K/V read stream, where write-back traffic is the costlier (measured: 256 sequences of
 // 1k-8k keys, 33.5 MB bound, 0.800 -> 0.778 ms with write-through; 128 sequences, 16.8 MB
-// bound, 114 -> 117 us, cfg3's decode part 221 -> 226 us).
+// bound, 114 -> 117 us; 128 sequences of 512-4096 keys, 221 -> 226 us).
 constexpr int64_t kStoreThroughBytes = 24ll << 20;
 
 // Slot of head_dim element d in a head's partial numerator row: lane c of the split kernel
