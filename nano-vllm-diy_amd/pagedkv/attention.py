@@ -55,5 +55,5 @@ class Attention(nn.Module):
             softmax_scale=self.scale,
             causal=True,
             block_table=ctx.block_tables,
-            cached_prefix_keys=ctx.cached_prefix_keys,
+            cached_prefix_keys=getattr(ctx, "cached_prefix_keys", None),  # absent on the reference Context
         )

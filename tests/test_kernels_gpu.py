@@ -417,3 +417,32 @@ def test_cache_hint_never_changes_results(gpu, name, num_seqs):
     torch.cuda.synchronize()
     for o in outs:
         assert bits_equal(o, ref)
+
+
+def test_attention_forward_accepts_reference_context(gpu):
+    """The layer takes the reference's eight-field Context (no cache hint) and gives the
+    same output as with this package's Context."""
+    import dataclasses
+
+    @dataclasses.dataclass
+    class RefContext:  # the fields of src/utils/context.py:5-14
+        is_prefill: bool = False
+        cu_seqlens_q: torch.Tensor | None = None
+        cu_seqlens_k: torch.Tensor | None = None
+        max_seqlen_q: int = 0
+        max_seqlen_k: int = 0
+        slot_mapping: torch.Tensor | None = None
+        context_lens: torch.Tensor | None = None
+        block_tables: torch.Tensor | None = None
+
+    w = make_workload("cfg4", gpu)
+    c = w.ctx
+    ref_ctx = RefContext(c.is_prefill, c.cu_seqlens_q, c.cu_seqlens_k, c.max_seqlen_q, c.max_seqlen_k,
+                         c.slot_mapping, c.context_lens, c.block_tables)
+    kc0, vc0 = w.k_cache.clone(), w.v_cache.clone()
+    out_a = _layer(w)(w.q, w.k, w.v, ref_ctx)
+    w.k_cache.copy_(kc0)
+    w.v_cache.copy_(vc0)
+    out_b = _layer(w)(w.q, w.k, w.v, c)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
