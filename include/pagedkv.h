@@ -188,6 +188,32 @@ int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride,
                             int32_t cached_prefix_keys, pk_stream_t stream);
 
 /*
+ * pk_store_decode_attention -- Attention.forward (attention.py:79-105) on a decode step in
+ * one split-K launch: store_kvcache of the tokens' key / value rows (attention.py:87-88,
+ * the contract of pk_store_kvcache) followed by paged decode attention
+ * (pk_varlen_attention_ex with max_seqlen_q = 1). No counterpart in the reference as one
+ * call; results, output and caches, are bit-identical to the two calls. Every sequence has
+ * one query row (row i of q, key and value is sequence i's token; graph padding rows: 0 or
+ * fewer keys and slot -1) and slot_mapping[i] is the cache slot of sequence i's last key.
+ */
+int pk_store_decode_attention(const void* q, int64_t q_row_stride,
+                              const void* key, int64_t key_row_stride,
+                              const void* value, int64_t value_row_stride,
+                              void* k_cache, void* v_cache,
+                              int64_t k_row_stride, int64_t v_row_stride,
+                              int64_t k_block_stride, int64_t v_block_stride,
+                              const int32_t* slot_mapping, int64_t num_slots,
+                              const int32_t* block_table, int32_t block_table_stride,
+                              int32_t block_size,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              int32_t num_seqs, int32_t max_seqlen_k,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              float softmax_scale,
+                              void* out, int64_t out_row_stride,
+                              void* workspace, size_t workspace_bytes,
+                              int32_t cached_prefix_keys, pk_stream_t stream);
+
+/*
  * Bytes of workspace pk_varlen_attention needs for these launch bounds: the
  * split-K partial outputs of the decode kernel (none when every sequence fits
  * one split) and, when max_seqlen_q > 1, the prefill work plan (work list,

@@ -115,7 +115,7 @@ int check_linear(const char* what, const void* x, int64_t x_row_stride, const vo
 
 extern "C" {
 
-int pk_abi_version(void) { return 6; }
+int pk_abi_version(void) { return 7; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -204,6 +204,10 @@ struct FusedProducer {
   float eps;
   const int32_t* slot_mapping;
   int64_t num_slots;
+  const void* new_k;            // store + decode: the tokens' K / V rows (qkv == nullptr)
+  int64_t new_k_stride;
+  const void* new_v;
+  int64_t new_v_stride;
 };
 
 // Shared body of pk_varlen_attention_ex and pk_qkv_decode_attention (fp != nullptr: q comes
@@ -228,7 +232,7 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   if (group != 1 && group != 2 && group != 4 && group != 8)
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: GQA group %d not built (1, 2, 4, 8)", group);
   if (num_seqs == 0 || max_seqlen_q == 0 || max_seqlen_k == 0) return PK_OK;
-  if ((!q && !fp) || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k)
+  if ((!q && !(fp && fp->qkv)) || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k)
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: null pointer argument");
   // the prefill work list packs key-tile indices in 16 bits and the kv head in 8
   if (max_seqlen_k > kMaxSeqlen || max_seqlen_q > kMaxSeqlen)
@@ -238,7 +242,7 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: num_kv_heads=%d above 255", num_kv_heads);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: q/k/v/out must be 16-byte aligned");
-  if (fp) q_row_stride = (int64_t)num_heads * head_dim;  // unused: q comes from qkv
+  if (fp && fp->qkv) q_row_stride = (int64_t)num_heads * head_dim;  // unused: q comes from qkv
   const int64_t kv_row = (int64_t)num_kv_heads * head_dim;
   if (q_row_stride < (int64_t)num_heads * head_dim || out_row_stride < (int64_t)num_heads * head_dim ||
       k_row_stride < kv_row || v_row_stride < kv_row)
@@ -310,6 +314,10 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
     a.norm_eps = fp->eps;
     a.slot_mapping = fp->slot_mapping;
     a.num_slots = fp->num_slots;
+    a.new_k = static_cast<const uint16_t*>(fp->new_k);
+    a.new_k_stride = fp->new_k_stride;
+    a.new_v = static_cast<const uint16_t*>(fp->new_v);
+    a.new_v_stride = fp->new_v_stride;
   }
   a.split_tokens = ws.split_tokens;
   a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
@@ -381,11 +389,40 @@ int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride, const int64
       (k_norm_weight && !aligned16(k_norm_weight)))
     return fail(PK_ERR_INVALID_ARG, "qkv_decode_attention: qkv / cos_sin / norm weights must be 16-byte aligned");
   const FusedProducer fp{qkv, qkv_row_stride, positions, cos_sin, max_position, q_norm_weight, k_norm_weight,
-                         eps, slot_mapping, num_slots};
+                         eps, slot_mapping, num_slots, nullptr, 0, nullptr, 0};
   return attention_impl(nullptr, 0, k_cache, v_cache, k_row_stride, v_row_stride, k_block_stride, v_block_stride,
                         block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs, 1,
                         max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, 1, out, out_row_stride,
                         workspace, workspace_bytes, cached_prefix_keys, &fp, stream);
+}
+
+int pk_store_decode_attention(const void* q, int64_t q_row_stride, const void* key, int64_t key_row_stride,
+                              const void* value, int64_t value_row_stride, void* k_cache, void* v_cache,
+                              int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                              int64_t v_block_stride, const int32_t* slot_mapping, int64_t num_slots,
+                              const int32_t* block_table, int32_t block_table_stride, int32_t block_size,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                              int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              float softmax_scale, void* out, int64_t out_row_stride, void* workspace,
+                              size_t workspace_bytes, int32_t cached_prefix_keys, pk_stream_t stream) {
+  g_last_error.clear();
+  if (num_seqs <= 0 || max_seqlen_k <= 0) return num_seqs < 0 || max_seqlen_k < 0 ?
+      fail(PK_ERR_INVALID_ARG, "store_decode_attention: negative num_seqs / max_seqlen_k") : PK_OK;
+  if (!key || !value || !slot_mapping || !block_table)
+    return fail(PK_ERR_INVALID_ARG, "store_decode_attention: null key / value / slot_mapping / block_table");
+  if (num_slots < 0) return fail(PK_ERR_INVALID_ARG, "store_decode_attention: num_slots < 0");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (key_row_stride < row || value_row_stride < row || key_row_stride % 8 || value_row_stride % 8)
+    return fail(PK_ERR_INVALID_ARG, "store_decode_attention: key/value row strides must be >= %lld and multiples of 8",
+                (long long)row);
+  if (!aligned16(key) || !aligned16(value))
+    return fail(PK_ERR_INVALID_ARG, "store_decode_attention: key / value must be 16-byte aligned");
+  const FusedProducer fp{nullptr, 0, nullptr, nullptr, 0, nullptr, nullptr, 0.f, slot_mapping, num_slots,
+                         key, key_row_stride, value, value_row_stride};
+  return attention_impl(q, q_row_stride, k_cache, v_cache, k_row_stride, v_row_stride, k_block_stride,
+                        v_block_stride, block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k,
+                        num_seqs, 1, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, 1, out,
+                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, &fp, stream);
 }
 
 int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,

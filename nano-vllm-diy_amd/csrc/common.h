@@ -73,6 +73,13 @@ struct AttnArgs {
   float norm_eps;
   const int32_t* slot_mapping;
   int64_t num_slots;            // > 0: slots outside [0, num_slots) are not written
+  // Fused store + decode (new_k != nullptr, qkv == nullptr): q comes from `q`, and the
+  // token's K and V rows from new_k / new_v (row = the token's index) go to slot_mapping
+  // unchanged, as store_kvcache writes them.
+  const uint16_t* new_k;
+  int64_t new_k_stride;
+  const uint16_t* new_v;
+  int64_t new_v_stride;
 };
 
 // Prefill plan sizes. The kernel runs kPrefillSlotsMax persistent work-groups at most (one

@@ -253,9 +253,10 @@ __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs&
 
 // Fused decode step: q of this DPP row's kv head g (its G query heads) is the RMSNorm +
 // RoPE of the token's fused qkv row, computed here exactly as the producer kernel computes
-// it (norm_rope.h). The split holding the sequence's last key -- the token itself, which
-// attends to its own key (attention.py:87-88 stores before attending) -- first writes the
-// token's normalised + rotated K row and raw V row of kv head g into the cache slot, and
+// it (norm_rope.h) -- or, for the fused store + decode, q as given. The split holding the
+// sequence's last key -- the token itself, which attends to its own key (attention.py:87-88
+// stores before attending) -- first writes the token's K row (normalised + rotated from qkv,
+// or as given) and V row of kv head g into the cache slot, and
 // waits for those stores before any K/V load: the same wavefront reads that row back in
 // its last pipeline step, and no other work-group reads it. The slot must be the cache
 // position of the sequence's last key (as the runner builds slot_mapping, model_runner.py:
@@ -264,36 +265,53 @@ template <int G>
 __device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>& st, int q0, int g, int c,
                                                bool row_live, bool stores_token) {
   constexpr int D = kHeadDim;
-  const bool lower = c < kLanesPerRow / 2;
-  float cv[8], sv[8];
-  rope_cos_sin_row(a.cos_sin, a.max_position, a.positions[q0], c, cv, sv);
-  const uint16_t* row = a.qkv + (int64_t)q0 * a.qkv_row_stride + c * 8;
-  uint4 w[G];
-#pragma unroll
-  for (int i = 0; i < G; ++i) w[i] = *reinterpret_cast<const uint4*>(row + (g * G + i) * D);
   int32_t slot = -1;
   uint4 wk, wv;
   if (stores_token) {
     slot = a.slot_mapping[q0];
     if (slot < 0 || (a.num_slots > 0 && (int64_t)slot >= a.num_slots)) slot = -1;
-    wk = *reinterpret_cast<const uint4*>(row + (a.num_heads + g) * D);
-    wv = *reinterpret_cast<const uint4*>(row + (a.num_heads + a.num_kv_heads + g) * D);
   }
+  if (a.qkv != nullptr) {
+    const bool lower = c < kLanesPerRow / 2;
+    float cv[8], sv[8];
+    rope_cos_sin_row(a.cos_sin, a.max_position, a.positions[q0], c, cv, sv);
+    const uint16_t* row = a.qkv + (int64_t)q0 * a.qkv_row_stride + c * 8;
+    uint4 w[G];
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const uint4 o = norm_rope_row(w[i], a.q_norm, a.norm_eps, cv, sv, lower, c);
-    st.qp[i][0] = o.x;
-    st.qp[i][1] = o.y;
-    st.qp[i][2] = o.z;
-    st.qp[i][3] = o.w;
+    for (int i = 0; i < G; ++i) w[i] = *reinterpret_cast<const uint4*>(row + (g * G + i) * D);
+    if (stores_token) {
+      wk = *reinterpret_cast<const uint4*>(row + (a.num_heads + g) * D);
+      wv = *reinterpret_cast<const uint4*>(row + (a.num_heads + a.num_kv_heads + g) * D);
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const uint4 o = norm_rope_row(w[i], a.q_norm, a.norm_eps, cv, sv, lower, c);
+      st.qp[i][0] = o.x;
+      st.qp[i][1] = o.y;
+      st.qp[i][2] = o.z;
+      st.qp[i][3] = o.w;
+    }
+    if (slot >= 0) wk = norm_rope_row(wk, a.k_norm, a.norm_eps, cv, sv, lower, c);
+  } else {  // store + decode: q as given, the raw K / V rows of the token (attention.py:27-34)
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const uint4 w = *reinterpret_cast<const uint4*>(a.q + (int64_t)q0 * a.q_row_stride + (g * G + i) * D + c * 8);
+      st.qp[i][0] = w.x;
+      st.qp[i][1] = w.y;
+      st.qp[i][2] = w.z;
+      st.qp[i][3] = w.w;
+    }
+    if (slot >= 0) {
+      wk = *reinterpret_cast<const uint4*>(a.new_k + (int64_t)q0 * a.new_k_stride + g * D + c * 8);
+      wv = *reinterpret_cast<const uint4*>(a.new_v + (int64_t)q0 * a.new_v_stride + g * D + c * 8);
+    }
   }
   if (slot >= 0) {  // uniform over the work-group: one token per sequence
-    const uint4 ok = norm_rope_row(wk, a.k_norm, a.norm_eps, cv, sv, lower, c);
     if (row_live) {
       const int64_t blk = slot / a.block_size, off = slot - blk * a.block_size;
       uint16_t* kd = const_cast<uint16_t*>(a.k) + blk * a.k_block_stride + off * a.k_row_stride + g * D + c * 8;
       uint16_t* vd = const_cast<uint16_t*>(a.v) + blk * a.v_block_stride + off * a.v_row_stride + g * D + c * 8;
-      *reinterpret_cast<uint4*>(kd) = ok;
+      *reinterpret_cast<uint4*>(kd) = wk;
       *reinterpret_cast<uint4*>(vd) = wv;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stores are done; no load moves above
@@ -513,7 +531,7 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const int zgroups = quads / waves;
   const dim3 grid((unsigned)(a.max_splits * a.num_seqs), (unsigned)zgroups);
   const dim3 block((unsigned)(waves * kWave));
-  if (a.qkv != nullptr)  // the fused decode step is paged only (checked by its entry point)
+  if (a.qkv != nullptr || a.new_k != nullptr)  // fused steps are paged only (checked by their entry points)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);
   else if (paged)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, block, 0, stream, a);

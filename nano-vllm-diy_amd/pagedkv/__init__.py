@@ -16,6 +16,7 @@ from .attention import Attention, store_kvcache  # noqa: F401
 from .context import Context  # noqa: F401
 from .ops import (add_rmsnorm, gather_kv, linear, linear_add_rmsnorm,  # noqa: F401
                   linear_silu_mul, linear_workspace_bytes, lm_head_greedy, qk_norm_rope_store, qkv_decode_attention,
+                  store_decode_attention,
                   reserve_linear_workspace, reserve_workspace, rope_cos_sin, shared_prefix_keys,
                   silu_and_mul, varlen_attention, workspace_bytes)
 
@@ -23,4 +24,4 @@ __all__ = ["Attention", "store_kvcache", "Context", "varlen_attention", "gather_
            "workspace_bytes", "reserve_workspace", "qk_norm_rope_store", "rope_cos_sin",
            "add_rmsnorm", "silu_and_mul", "lm_head_greedy", "linear", "linear_silu_mul",
            "linear_add_rmsnorm", "linear_workspace_bytes", "reserve_linear_workspace",
-           "shared_prefix_keys", "qkv_decode_attention"]
+           "shared_prefix_keys", "qkv_decode_attention", "store_decode_attention"]

@@ -62,6 +62,20 @@ SIGNATURES = {
         _c_void_p, _i64,                    # out, out_row_stride
         _c_void_p, _size_t,                 # workspace, its bytes
         _i32, _c_void_p]),                  # cached_prefix_keys, stream
+    "pk_store_decode_attention": (ctypes.c_int, [
+        _c_void_p, _i64,                    # q, q_row_stride
+        _c_void_p, _i64, _c_void_p, _i64,   # key, its row stride, value, its row stride
+        _c_void_p, _c_void_p,               # k_cache, v_cache
+        _i64, _i64, _i64, _i64,             # k/v row strides, k/v block strides
+        _c_void_p, _i64,                    # slot_mapping, num_slots
+        _c_void_p, _i32, _i32,              # block_table, its row stride, block_size
+        _c_void_p, _c_void_p,               # cu_seqlens_q, cu_seqlens_k
+        _i32, _i32,                         # num_seqs, max_seqlen_k
+        _i32, _i32, _i32,                   # num_heads, num_kv_heads, head_dim
+        ctypes.c_float,                     # softmax_scale
+        _c_void_p, _i64,                    # out, out_row_stride
+        _c_void_p, _size_t,                 # workspace, its bytes
+        _i32, _c_void_p]),                  # cached_prefix_keys, stream
     "pk_varlen_attention_workspace_bytes": (_size_t, [_i32, _i32, _i32, _i32, _i32]),
     "pk_gather_kv": (ctypes.c_int, [
         _c_void_p, _i64, _i32, _c_void_p, _i32, _c_void_p, _i32, _i32, _i32, _c_void_p,
@@ -95,7 +109,7 @@ SIGNATURES = {
         _c_void_p, _size_t, _c_void_p]),    # workspace, workspace_bytes, stream
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

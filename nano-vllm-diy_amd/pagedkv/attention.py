@@ -9,7 +9,9 @@ every device operation is a hand-written gfx950 HIP kernel from libpagedkv.so:
 * with ctx.block_tables set it reads K/V from the paged cache, otherwise from the
   fresh k / v rows (attention.py:93-94);
 * one call covers a mixed batch: one-row sequences go to the split-K decode kernel
-  and longer ones to the MFMA prefill kernel, both bottom-right causal.
+  and longer ones to the MFMA prefill kernel, both bottom-right causal;
+* on a decode step (one new token per sequence, paged) the store and the attention run
+  in one launch of the split-K kernel (pk_store_decode_attention), bit-identical to the two.
 
 The runner rebinds k_cache / v_cache to per-layer views of its KV tensor
 (model_runner.py:159-165), exactly as with the reference layer.
@@ -21,7 +23,7 @@ from torch import nn
 
 from .context import Context
 from .ops import store_kvcache as _store_kvcache
-from .ops import varlen_attention
+from .ops import store_decode_attention, varlen_attention
 
 
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
@@ -42,7 +44,16 @@ class Attention(nn.Module):
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ctx: Context) -> torch.Tensor:
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
+        bound = k_cache.numel() and v_cache.numel()
+        hint = getattr(ctx, "cached_prefix_keys", None)  # absent on the reference Context
+        if bound and ctx.block_tables is not None and ctx.max_seqlen_q == 1 and \
+                q.shape[0] == k.shape[0] == ctx.cu_seqlens_q.numel() - 1:
+            # a decode step (one new token per sequence): the store and the attention in one
+            # launch, bit-identical to the two
+            return store_decode_attention(q, k, v, k_cache, v_cache, ctx.slot_mapping, ctx.cu_seqlens_q,
+                                          ctx.cu_seqlens_k, ctx.max_seqlen_k, self.scale, ctx.block_tables,
+                                          cached_prefix_keys=hint)
+        if bound:
             store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
         if ctx.block_tables is not None:
             k, v = k_cache, v_cache
@@ -55,5 +66,5 @@ class Attention(nn.Module):
             softmax_scale=self.scale,
             causal=True,
             block_table=ctx.block_tables,
-            cached_prefix_keys=getattr(ctx, "cached_prefix_keys", None),  # absent on the reference Context
+            cached_prefix_keys=hint,
         )

@@ -287,6 +287,70 @@ def qkv_decode_attention(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: to
     return out
 
 
+def store_decode_attention(q: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                           k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                           cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_k: int,
+                           softmax_scale: float | None, block_table: torch.Tensor,
+                           out: torch.Tensor | None = None, cached_prefix_keys: int | None = None,
+                           check_slots: bool = False, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention.forward on a decode step (src/layers/attention.py:87-104) in one launch:
+    the store of store_kvcache (same layout checks, attention.py:51-56) followed by paged
+    decode attention; output and caches are bit-identical to store_kvcache + varlen_attention.
+    Row i of q, key and value is sequence i's token (one query row per sequence) and
+    slot_mapping[i] is the cache slot of sequence i's last key. Returns out (S, Hq, D) bf16.
+    """
+    n, num_heads, head_dim = q.shape
+    num_kv_heads = key.shape[1]
+    row = num_kv_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == row and v_cache.stride(1) == row
+    assert slot_mapping.numel() == key.shape[0]
+    dev = q.device
+    if q.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16 or \
+            k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("q, key, value and caches must be bfloat16")
+    if value.shape != key.shape or key.shape[0] != n or key.shape[2] != head_dim:
+        raise ValueError("q (S, Hq, D), key / value (S, Hkv, D): one token per sequence")
+    if q.stride(-1) != 1 or q.stride(1) != head_dim:
+        raise ValueError("q must have contiguous heads")
+    for c in (k_cache, v_cache):
+        if c.dim() != 4 or c.device != dev or c.stride(-1) != 1 or c.stride(-2) != head_dim or \
+                c.shape[-2] != num_kv_heads:
+            raise ValueError("caches must be (NB, BS, Hkv, D) bf16 with contiguous heads")
+    for name, t in (("key", key), ("value", value)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    _req_i32("slot_mapping", slot_mapping, dev)
+    _req_i32("cu_seqlens_q", cu_seqlens_q, dev)
+    _req_i32("cu_seqlens_k", cu_seqlens_k, dev)
+    _req_i32("block_table", block_table, dev)
+    num_seqs = cu_seqlens_q.numel() - 1
+    if num_seqs != n or cu_seqlens_k.numel() != n + 1 or not slot_mapping.is_contiguous() or \
+            not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):
+        raise ValueError("a decode step has one row, one slot and one (q, k) length pair per sequence")
+    if block_table.dim() != 2 or block_table.stride(1) != 1 or block_table.shape[0] < num_seqs:
+        raise ValueError("block_table must be (S, W) with contiguous rows")
+    num_slots = k_cache.shape[0] * k_cache.shape[1] if check_slots else 0
+    if out is None:
+        out = torch.empty(n, num_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    elif out.shape != q.shape or out.dtype != torch.bfloat16 or out.stride(-1) != 1 or out.stride(1) != head_dim:
+        raise ValueError("out must be (S, Hq, D) bf16 with contiguous heads")
+    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    nbytes = workspace_bytes(num_seqs, num_heads, head_dim, 1, max_seqlen_k)
+    ws = _workspace(nbytes, dev) if workspace is None else _given_workspace(workspace, nbytes, dev)
+    hint = PK_CACHED_PREFIX_KEYS_DEFAULT if cached_prefix_keys is None else int(cached_prefix_keys)
+    check(lib().pk_store_decode_attention(
+        q.data_ptr(), q.stride(0), key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(1), v_cache.stride(1), k_cache.stride(0),
+        v_cache.stride(0), slot_mapping.data_ptr(), num_slots, block_table.data_ptr(), block_table.stride(0),
+        k_cache.shape[1], cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, int(max_seqlen_k),
+        num_heads, num_kv_heads, head_dim, scale, out.data_ptr(), out.stride(0),
+        ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0, hint, _stream(q)),
+        "pk_store_decode_attention")
+    return out
+
+
 def shared_prefix_keys(block_tables, block_size: int) -> int:
     """The cached_prefix_keys value for a batch: the longest run of leading blocks that
     some sequence shares with another (block reference count > 1, the count the

@@ -120,3 +120,30 @@ def test_fused_decode_in_graph_replays(gpu):
         a, _ = _both(b2, 16, 8, cs)
         assert torch.equal(a[0][:S].view(torch.int16), out[:S].view(torch.int16)), f"replay {r}"
         assert torch.equal(a[1].view(torch.int16), kcg.view(torch.int16)), f"replay {r}: K cache"
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (16, 4)])
+def test_store_decode_bit_identical_to_store_then_attention(gpu, hq, hkv):
+    """pk_store_decode_attention (Attention.forward on a decode step) against
+    pk_store_kvcache + pk_varlen_attention_ex: output and caches bit-identical, with graph
+    padding rows and a strided value view (as qwen3.py passes v)."""
+    b = _batch([1, 5, 255, 256, 257, 3000, 700], hq, hkv, seed=31 + hq, dev=gpu, pad=2)
+    S = b["S"]
+    g = torch.Generator().manual_seed(3)
+    n = S + 2
+    q = (torch.randn(n, hq, D, generator=g)).to(torch.bfloat16).to(gpu)
+    kv = (torch.randn(n, 2 * hkv * D + 64, generator=g)).to(torch.bfloat16).to(gpu)
+    key = kv[:, :hkv * D].view(n, hkv, D)
+    value = kv[:, hkv * D:2 * hkv * D].view(n, hkv, D)          # row stride 2 hkv D + 64
+    scale = D ** -0.5
+    kca, vca = b["kc"].clone(), b["vc"].clone()
+    pagedkv.store_kvcache(key, value, kca, vca, b["slot"])
+    out_a = pagedkv.varlen_attention(q, kca, vca, b["cu_q"], b["cu_k"], 1, b["maxk"], scale, True, b["bt"],
+                                     cached_prefix_keys=0)
+    kcb, vcb = b["kc"].clone(), b["vc"].clone()
+    layer = pagedkv.Attention(D, hq, hkv, scale)
+    layer.k_cache, layer.v_cache = kcb, vcb
+    ctx = pagedkv.Context(False, b["cu_q"], b["cu_k"], 1, b["maxk"], b["slot"], None, b["bt"], 0)
+    out_b = layer(q, key, value, ctx)
+    torch.cuda.synchronize()
+    _assert_same((out_a, kca, vca), (out_b, kcb, vcb), S)
