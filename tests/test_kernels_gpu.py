@@ -321,6 +321,36 @@ def test_graph_capture_padded_decode_replay(gpu):
     assert bits_equal(w.k_cache, cache_before[0]) and bits_equal(w.v_cache, cache_before[1])
 
 
+def test_graph_capture_mixed_call_replay(gpu):
+    """A call with both decode and prefill sequences (decode split + combine, prefill plan +
+    persistent prefill + merge) captured into a graph: every replay is bit-identical to the
+    eager call, with eager calls of the same shape in between."""
+    w = make_workload("cfg3", gpu, num_seqs=24)
+    assert 1 in w.q_lens and max(w.q_lens) > 1
+    ws = torch.empty(pagedkv.workspace_bytes(len(w.q_lens), 16, 128, w.max_seqlen_q, w.max_seqlen_k),
+                     dtype=torch.uint8, device=gpu)
+
+    def run():
+        return pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k,
+                                        w.max_seqlen_q, w.max_seqlen_k, None, True, w.block_tables,
+                                        workspace=ws)
+    want = run()
+    torch.cuda.synchronize()
+    print("[graph] cfg3 mixed call, 24 sequences", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_static = run()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out_static.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bits_equal(out_static, want), f"replay {rep}"
+        again = run()
+        torch.cuda.synchronize()
+        assert bits_equal(again, want), f"eager call after replay {rep}"
+
+
 def test_workspace_reuse_across_batch_shapes(gpu):
     """One shared workspace serves calls of different shapes in any order: each result is
     bit-identical to the same call on a fresh (zero-filled) workspace."""
