@@ -284,3 +284,36 @@ def test_fused_decode_argument_checks_fail_before_launch():
     assert _fused(lib) == _lib.PK_ERR_WORKSPACE
     assert _fused(lib, num_seqs=-1) == _lib.PK_ERR_INVALID_ARG
     assert _fused(lib, num_seqs=0) == _lib.PK_OK
+
+
+
+def _store_decode(lib, **kw):
+    fake = ctypes.c_void_p(0x10000)
+    row = HKV * HEAD_DIM
+    args = dict(q=fake, q_row_stride=HQ * HEAD_DIM, key=fake, key_row_stride=row, value=fake,
+                value_row_stride=4 * row, k_cache=fake, v_cache=fake, k_row_stride=row, v_row_stride=row,
+                k_block_stride=BLOCK_SIZE * row, v_block_stride=BLOCK_SIZE * row, slot_mapping=fake,
+                num_slots=0, block_table=fake, bt_stride=8, block_size=BLOCK_SIZE, cu_q=fake, cu_k=fake,
+                num_seqs=2, max_k=2048, num_heads=HQ, num_kv_heads=HKV, head_dim=HEAD_DIM, scale=0.088,
+                out=fake, out_row_stride=HQ * HEAD_DIM, ws=None, ws_bytes=0, hint=0, stream=None)
+    args.update(kw)
+    return lib.pk_store_decode_attention(*args.values())
+
+
+def test_store_decode_argument_checks_fail_before_launch():
+    """pk_store_decode_attention refuses bad arguments on the host, before any launch."""
+    lib = _lib.lib()
+    assert _store_decode(lib, key=None) == _lib.PK_ERR_INVALID_ARG
+    assert b"null" in lib.pk_last_error()
+    assert _store_decode(lib, q=None) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib, block_table=None) == _lib.PK_ERR_INVALID_ARG     # paged only
+    assert _store_decode(lib, key_row_stride=HKV * HEAD_DIM - 8) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib, value_row_stride=HKV * HEAD_DIM + 4) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib, value=ctypes.c_void_p(0x10008)) == _lib.PK_ERR_INVALID_ARG
+    assert b"aligned" in lib.pk_last_error()
+    assert _store_decode(lib, num_slots=-1) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib, head_dim=64) == _lib.PK_ERR_UNSUPPORTED
+    assert _store_decode(lib, block_size=100) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib) == _lib.PK_ERR_WORKSPACE    # split-K partials need a workspace
+    assert _store_decode(lib, num_seqs=-1) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib, num_seqs=0) == _lib.PK_OK
