@@ -430,6 +430,11 @@ def extra_configs(dev, w2):
     wd = make_workload("cfg1_decode", dev)
     ms, _ = timed_launches(attention_call(wd), 20)
     res["cfg1_decode"] = {"ms": round(ms, 5), "GB/s": round(wd.decode_kv_bytes() / ms / 1e6, 1)}
+    # the drop-in's decode step (store + decode): Attention.forward does both in one launch
+    fwd = pagedkv.Attention(128, 16, 8, SCALE)
+    fwd.k_cache, fwd.v_cache = wd.k_cache, wd.v_cache
+    ms, _ = timed_launches(lambda: fwd(wd.q, wd.k, wd.v, wd.ctx), 20)
+    res["cfg1_forward_step"] = {"ms": round(ms, 5), "GB/s": round(wd.decode_kv_bytes() / ms / 1e6, 1)}
 
     log("[bench] cfg3")
     w3 = make_workload("cfg3", dev)
