@@ -169,6 +169,15 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride,
  * rows: 0 or fewer keys and slot -1). slot_mapping[i] must be the cache slot of the last
  * key of sequence i (the token's own position), as the runner builds it: the key is
  * written there and read back through the block table by the same wavefront.
+ * Preconditions of the one launch (checked where the host can: PK_ERR_INVALID_ARG):
+ *   - the caches have contiguous rows and blocks (k_row_stride == num_kv_heads * head_dim,
+ *     k_block_stride == block_size * k_row_stride, the same for v), so the row lands where
+ *     pk_qk_norm_rope_store writes it (slot * row);
+ *   - no other sequence of the batch reads the cache block holding slot_mapping[i]: the
+ *     row is written while other work-groups of the launch read the cache, unordered with
+ *     their reads. With prefix caching a fully cached prompt recomputes its last token into
+ *     a shared block (src/engine/scheduler.py:77-80, model_runner.py:185-186); such a batch
+ *     must use the two calls, whose store is ordered before every read.
  */
 int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride,
                             const int64_t* positions, const float* cos_sin, int64_t max_position,
@@ -195,6 +204,10 @@ int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride,
  * call; results, output and caches, are bit-identical to the two calls. Every sequence has
  * one query row (row i of q, key and value is sequence i's token; graph padding rows: 0 or
  * fewer keys and slot -1) and slot_mapping[i] is the cache slot of sequence i's last key.
+ * Same two preconditions as pk_qkv_decode_attention: contiguous cache rows and blocks
+ * (the row lands where pk_store_kvcache writes it, slot * row), and no other sequence of
+ * the batch reads the block holding slot_mapping[i]. pagedkv.Attention takes this path
+ * only when its Context states that no block is shared (cached_prefix_keys == 0).
  */
 int pk_store_decode_attention(const void* q, int64_t q_row_stride,
                               const void* key, int64_t key_row_stride,

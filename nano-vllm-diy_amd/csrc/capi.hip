@@ -82,6 +82,24 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
   return w;
 }
 
+// The one-launch decode steps write the token's row at block * block_stride + offset *
+// row_stride, where pk_store_kvcache / pk_qk_norm_rope_store write at slot * row: the two
+// agree only for caches whose rows and blocks are contiguous, which both entry points
+// therefore require (the reference's runner allocates the cache that way,
+// model_runner.py:159-165, and asserts the row stride, attention.py:53).
+int check_contiguous_cache(const char* what, int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                           int64_t v_block_stride, int32_t block_size, int32_t num_kv_heads, int32_t head_dim) {
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (k_row_stride != row || v_row_stride != row || k_block_stride != (int64_t)block_size * row ||
+      v_block_stride != (int64_t)block_size * row)
+    return fail(PK_ERR_INVALID_ARG,
+                "%s: caches must have contiguous rows and blocks (row stride %lld, block stride %lld; got %lld/%lld, "
+                "%lld/%lld)",
+                what, (long long)row, (long long)block_size * row, (long long)k_row_stride, (long long)v_row_stride,
+                (long long)k_block_stride, (long long)v_block_stride);
+  return PK_OK;
+}
+
 // Shared argument checks of the decode-step linear entry points; 0 when valid.
 int check_linear(const char* what, const void* x, int64_t x_row_stride, const void* weight,
                  int64_t weight_row_stride, int32_t rows, int32_t n_out, int32_t k,
@@ -267,6 +285,12 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   }
   if (!(softmax_scale > 0.f) || !std::isfinite(softmax_scale))
     return fail(PK_ERR_INVALID_ARG, "varlen_attention: softmax_scale must be positive and finite");
+  if (fp) {  // a one-launch decode step stores into the cache it reads
+    if (int rc = check_contiguous_cache(fp->qkv ? "qkv_decode_attention" : "store_decode_attention", k_row_stride,
+                                        v_row_stride, k_block_stride, v_block_stride, block_size, num_kv_heads,
+                                        head_dim))
+      return rc;
+  }
 
   const WorkspaceLayout ws = workspace_layout(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k);
   if (ws.total > 0) {

@@ -262,6 +262,8 @@ def qkv_decode_attention(qkv: torch.Tensor, positions: torch.Tensor, cos_sin: to
         if c.dim() != 4 or c.dtype != torch.bfloat16 or c.device != dev or c.stride(-1) != 1 or \
                 c.stride(-2) != head_dim or c.shape[-2] != num_kv_heads or c.shape[-1] != head_dim:
             raise ValueError("caches must be (NB, BS, Hkv, D) bf16 with contiguous heads")
+        if c.stride(1) != row or c.stride(0) != c.shape[1] * row:
+            raise ValueError("qkv_decode_attention needs caches with contiguous rows and blocks")
     if v_cache.shape != k_cache.shape:
         raise ValueError("k_cache and v_cache shapes differ")
     num_slots = k_cache.shape[0] * k_cache.shape[1] if check_slots else 0
@@ -297,7 +299,10 @@ def store_decode_attention(q: torch.Tensor, key: torch.Tensor, value: torch.Tens
     the store of store_kvcache (same layout checks, attention.py:51-56) followed by paged
     decode attention; output and caches are bit-identical to store_kvcache + varlen_attention.
     Row i of q, key and value is sequence i's token (one query row per sequence) and
-    slot_mapping[i] is the cache slot of sequence i's last key. Returns out (S, Hq, D) bf16.
+    slot_mapping[i] is the cache slot of sequence i's last key, in a cache block that no other
+    sequence of the batch reads (the row is written while other work-groups read the cache;
+    with shared prefix blocks call store_kvcache + varlen_attention instead). The caches'
+    rows and blocks must be contiguous. Returns out (S, Hq, D) bf16.
     """
     n, num_heads, head_dim = q.shape
     num_kv_heads = key.shape[1]
@@ -318,6 +323,11 @@ def store_decode_attention(q: torch.Tensor, key: torch.Tensor, value: torch.Tens
         if c.dim() != 4 or c.device != dev or c.stride(-1) != 1 or c.stride(-2) != head_dim or \
                 c.shape[-2] != num_kv_heads:
             raise ValueError("caches must be (NB, BS, Hkv, D) bf16 with contiguous heads")
+        if c.stride(0) != c.shape[1] * row:
+            # the one launch writes the token row at block * block_stride + offset * row, where
+            # store_kvcache writes slot * row: the same place only for contiguous blocks
+            raise ValueError("store_decode_attention needs caches with contiguous blocks "
+                             "(stride(0) == block_size * Hkv * D); use store_kvcache + varlen_attention")
     for name, t in (("key", key), ("value", value)):
         if t.device != dev:
             raise ValueError(f"{name} is on {t.device}, expected {dev}")

@@ -280,6 +280,10 @@ def test_fused_decode_argument_checks_fail_before_launch():
     assert _fused(lib, head_dim=64) == _lib.PK_ERR_UNSUPPORTED
     assert _fused(lib, num_heads=24, qkv_row_stride=(24 + 2 * HKV) * HEAD_DIM) == _lib.PK_ERR_UNSUPPORTED  # GQA 3
     assert _fused(lib, block_size=100) == _lib.PK_ERR_INVALID_ARG
+    # the token row is written at block * block_stride + offset * row: contiguous caches only
+    assert _fused(lib, k_block_stride=2 * BLOCK_SIZE * HKV * HEAD_DIM) == _lib.PK_ERR_INVALID_ARG
+    assert b"contiguous" in lib.pk_last_error()
+    assert _fused(lib, v_row_stride=2 * HKV * HEAD_DIM) == _lib.PK_ERR_INVALID_ARG
     # the split-K partials need a workspace: refused before any launch
     assert _fused(lib) == _lib.PK_ERR_WORKSPACE
     assert _fused(lib, num_seqs=-1) == _lib.PK_ERR_INVALID_ARG
@@ -314,6 +318,24 @@ def test_store_decode_argument_checks_fail_before_launch():
     assert _store_decode(lib, num_slots=-1) == _lib.PK_ERR_INVALID_ARG
     assert _store_decode(lib, head_dim=64) == _lib.PK_ERR_UNSUPPORTED
     assert _store_decode(lib, block_size=100) == _lib.PK_ERR_INVALID_ARG
+    assert _store_decode(lib, v_block_stride=2 * BLOCK_SIZE * HKV * HEAD_DIM) == _lib.PK_ERR_INVALID_ARG
+    assert b"contiguous" in lib.pk_last_error()
+    assert _store_decode(lib, k_row_stride=2 * HKV * HEAD_DIM,
+                         k_block_stride=2 * BLOCK_SIZE * HKV * HEAD_DIM) == _lib.PK_ERR_INVALID_ARG
     assert _store_decode(lib) == _lib.PK_ERR_WORKSPACE    # split-K partials need a workspace
     assert _store_decode(lib, num_seqs=-1) == _lib.PK_ERR_INVALID_ARG
     assert _store_decode(lib, num_seqs=0) == _lib.PK_OK
+
+def test_attention_takes_one_launch_only_over_unshared_contiguous_blocks():
+    """Attention.forward's decode-step dispatch: the one-launch store + decode needs caches
+    with contiguous blocks and a Context that states no block is shared
+    (cached_prefix_keys == 0); anything else takes store_kvcache + varlen_attention."""
+    from pagedkv.attention import _contiguous_blocks
+
+    kc = torch.empty(4, BLOCK_SIZE, HKV, HEAD_DIM, dtype=torch.bfloat16)
+    assert _contiguous_blocks(kc)
+    big = torch.empty(4, 2 * BLOCK_SIZE, HKV, HEAD_DIM, dtype=torch.bfloat16)
+    assert not _contiguous_blocks(big[:, :BLOCK_SIZE])           # padded blocks
+    both = torch.empty(2, 4, BLOCK_SIZE, HKV, HEAD_DIM, dtype=torch.bfloat16)
+    assert _contiguous_blocks(both[0]) and _contiguous_blocks(both[1])   # the runner's per-layer views
+
