@@ -155,6 +155,41 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride,
                            int32_t cached_prefix_keys, pk_stream_t stream);
 
 /*
+ * pk_varlen_attention_noalloc -- pk_varlen_attention_ex for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments, semantics and kernels as
+ * pk_varlen_attention_ex -- outputs are bit-identical -- minus the workspace: the split-K
+ * partials and the prefill work plan live in a static device array of
+ * PK_NOALLOC_SCRATCH_BYTES (128 MiB) that each GPU the library runs on holds from the
+ * first call on it until the process ends. The call allocates nothing (no hipMalloc, no
+ * allocating library routine).
+ *   - Launch bounds whose pk_varlen_attention_workspace_bytes exceeds the scratch return
+ *     PK_ERR_WORKSPACE before any launch (every batch of the five benchmark shapes fits:
+ *     256 decode sequences of up to 8192 keys need 32.5 MiB, a mixed chunked-prefill batch
+ *     about 115 MiB).
+ *   - The stream must belong to the current device (PK_ERR_INVALID_ARG otherwise). The first
+ *     call on a device looks the array's address up (hipGetSymbolAddress): make it outside
+ *     graph capture.
+ *   - Every call on one GPU shares that GPU's array: calls that can overlap on one GPU
+ *     (two streams, two threads, concurrently replayed graphs) race and give wrong results.
+ *     Each call writes every scratch byte it reads first; no contents carry over.
+ */
+#define PK_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+int pk_varlen_attention_noalloc(const void* q, int64_t q_row_stride,
+                                const void* k, const void* v,
+                                int64_t k_row_stride, int64_t v_row_stride,
+                                int64_t k_block_stride, int64_t v_block_stride,
+                                const int32_t* block_table, int32_t block_table_stride,
+                                int32_t block_size,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                float softmax_scale, int32_t causal,
+                                void* out, int64_t out_row_stride,
+                                int32_t cached_prefix_keys, pk_stream_t stream);
+
+/*
  * pk_qkv_decode_attention -- one decode step of an attention layer from the fused qkv
  * projection, in one split-K launch (no counterpart in the reference: it is
  * pk_qk_norm_rope_store(qkv, ..., k_cache, v_cache, slot_mapping) followed by

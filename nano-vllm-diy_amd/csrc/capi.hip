@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/pagedkv.h"
@@ -133,7 +134,7 @@ int check_linear(const char* what, const void* x, int64_t x_row_stride, const vo
 
 extern "C" {
 
-int pk_abi_version(void) { return 7; }
+int pk_abi_version(void) { return 8; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -605,3 +606,73 @@ int pk_linear_add_rmsnorm(const void* x, int64_t x_row_stride, const void* weigh
 }
 
 }  // extern "C"
+
+// ---- allocation-free entry point --------------------------------------------------------
+// pk_varlen_attention_noalloc runs the kernels of pk_varlen_attention_ex on this file-scope
+// device array instead of a caller's workspace. Each GPU the library runs on holds its own
+// copy (PK_NOALLOC_SCRATCH_BYTES) from the first launch on it until the process ends. In host
+// code `scratch` names a host-side stand-in, not device memory: its device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only that address is
+// ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[PK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch` per device ordinal
+
+// Device address of the current device's scratch, looked up on its first use (no allocation).
+int device_scratch(pk_stream_t stream, void** out) {
+  int dev = -1;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e, "varlen_attention_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(PK_ERR_UNSUPPORTED, "varlen_attention_noalloc: device ordinal %d above %d", dev, kMaxDevices - 1);
+  if (stream != nullptr) {  // the kernels run on the stream's device: it must own this scratch
+    int sdev = -1;
+    if (hipError_t e = hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev); e != hipSuccess)
+      return hip_status(e, "varlen_attention_noalloc: hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(PK_ERR_INVALID_ARG, "varlen_attention_noalloc: stream belongs to device %d, current device is %d",
+                  sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+      return hip_status(e, "varlen_attention_noalloc: hipGetSymbolAddress(scratch)");
+    if (p == nullptr || (reinterpret_cast<uintptr_t>(p) % kWorkspaceAlign) != 0)
+      return fail(PK_ERR_HIP, "varlen_attention_noalloc: scratch address %p unusable", p);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PK_OK;
+}
+
+}  // namespace
+
+extern "C" int pk_varlen_attention_noalloc(const void* q, int64_t q_row_stride, const void* k, const void* v,
+                                           int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                                           int64_t v_block_stride, const int32_t* block_table,
+                                           int32_t block_table_stride, int32_t block_size,
+                                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                           int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                           float softmax_scale, int32_t causal, void* out, int64_t out_row_stride,
+                                           int32_t cached_prefix_keys, pk_stream_t stream) {
+  g_last_error.clear();
+  const size_t need = pk_varlen_attention_workspace_bytes(num_seqs, num_heads, head_dim, max_seqlen_q, max_seqlen_k);
+  if (need > (size_t)PK_NOALLOC_SCRATCH_BYTES)
+    return fail(PK_ERR_WORKSPACE,
+                "varlen_attention_noalloc: these launch bounds (num_seqs=%d, max_seqlen_q=%d, max_seqlen_k=%d) need "
+                "%zu bytes of scratch; the static scratch holds %zu (use pk_varlen_attention_ex with a workspace)",
+                num_seqs, max_seqlen_q, max_seqlen_k, need, (size_t)PK_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = device_scratch(stream, &ws)) return rc;
+  }
+  return attention_impl(q, q_row_stride, k, v, k_row_stride, v_row_stride, k_block_stride, v_block_stride, block_table,
+                        block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs, max_seqlen_q,
+                        max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, causal, out, out_row_stride,
+                        ws, need > 0 ? (size_t)PK_NOALLOC_SCRATCH_BYTES : 0, cached_prefix_keys, nullptr, stream);
+}

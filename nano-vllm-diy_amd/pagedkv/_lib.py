@@ -47,6 +47,12 @@ SIGNATURES = {
         _i32, _i32, _i32, ctypes.c_float, _i32, _c_void_p, _i64, _c_void_p, _size_t,
         _i32,                               # cached_prefix_keys
         _c_void_p]),                        # stream
+    "pk_varlen_attention_noalloc": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+        _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
+        _i32, _i32, _i32, ctypes.c_float, _i32, _c_void_p, _i64,
+        _i32,                               # cached_prefix_keys
+        _c_void_p]),                        # stream
     "pk_qkv_decode_attention": (ctypes.c_int, [
         _c_void_p, _i64,                    # qkv, qkv_row_stride
         _c_void_p, _c_void_p, _i64,         # positions, cos_sin, max_position
@@ -109,7 +115,7 @@ SIGNATURES = {
         _c_void_p, _size_t, _c_void_p]),    # workspace, workspace_bytes, stream
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -339,3 +339,22 @@ def test_attention_takes_one_launch_only_over_unshared_contiguous_blocks():
     both = torch.empty(2, 4, BLOCK_SIZE, HKV, HEAD_DIM, dtype=torch.bfloat16)
     assert _contiguous_blocks(both[0]) and _contiguous_blocks(both[1])   # the runner's per-layer views
 
+
+def test_no_alloc_refuses_bounds_beyond_its_scratch():
+    """pk_varlen_attention_noalloc checks its launch bounds against the static scratch on the
+    host: 2048 decode sequences of 8192 keys need 256 MiB of partials, above the 128 MiB, and
+    are refused before any device call."""
+    lib = _lib.lib()
+    need = lib.pk_varlen_attention_workspace_bytes(2048, HQ, HEAD_DIM, 1, 8192)
+    assert need > 128 << 20
+    assert lib.pk_varlen_attention_workspace_bytes(256, HQ, HEAD_DIM, 1, 8192) <= 128 << 20
+    fake = ctypes.c_void_p(0x10000)
+    row = HKV * HEAD_DIM
+    rc = lib.pk_varlen_attention_noalloc(fake, HQ * HEAD_DIM, fake, fake, row, row, BLOCK_SIZE * row,
+                                         BLOCK_SIZE * row, fake, 32, BLOCK_SIZE, fake, fake, 2048, 1, 8192,
+                                         HQ, HKV, HEAD_DIM, 0.088, 1, fake, HQ * HEAD_DIM, 0, None)
+    assert rc == _lib.PK_ERR_WORKSPACE
+    assert b"static scratch" in lib.pk_last_error()
+    # nothing to do: success without touching the device
+    assert lib.pk_varlen_attention_noalloc(None, HQ * HEAD_DIM, None, None, row, row, 0, 0, None, 0, 0, None, None,
+                                           0, 1, 1, HQ, HKV, HEAD_DIM, 0.088, 1, None, HQ * HEAD_DIM, 0, None) == 0

@@ -1,0 +1,59 @@
+"""GPU test of the allocation-free entry point pk_varlen_attention_noalloc (through the C-ABI):
+its output must be bit-identical to pk_varlen_attention_ex with a caller's workspace (the
+same kernels), on several calls in a row that share the static scratch -- a mixed
+chunked-prefill + decode batch, then smaller decode batches -- so nothing one call leaves in
+the scratch can change the next call's result."""
+import ctypes
+
+import pytest
+import torch
+
+from paged_helpers import bits_equal
+from pagedkv import _lib
+from pagedkv.workloads import make_workload
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 128 ** -0.5
+
+
+def _args(w, out):
+    return (w.q.data_ptr(), w.q.stride(0), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
+            w.k_cache.stride(1), w.v_cache.stride(1), w.k_cache.stride(0), w.v_cache.stride(0),
+            w.block_tables.data_ptr(), w.block_tables.stride(0), w.k_cache.shape[1],
+            w.cu_seqlens_q.data_ptr(), w.cu_seqlens_k.data_ptr(), len(w.q_lens), w.max_seqlen_q, w.max_seqlen_k,
+            16, 8, 128, SCALE, 1, out.data_ptr(), out.stride(0))
+
+
+def _with_workspace(w, hint):
+    lib = _lib.lib()
+    need = lib.pk_varlen_attention_workspace_bytes(len(w.q_lens), 16, 128, w.max_seqlen_q, w.max_seqlen_k)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=w.q.device)
+    out = torch.zeros_like(w.q)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.pk_varlen_attention_ex(*_args(w, out), ws.data_ptr(), need, hint, stream), "pk_varlen_attention_ex")
+    return out
+
+
+def _no_alloc(w, hint):
+    lib = _lib.lib()
+    out = torch.zeros_like(w.q)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.pk_varlen_attention_noalloc(*_args(w, out), hint, stream), "pk_varlen_attention_noalloc")
+    return out
+
+
+def test_no_alloc_matches_workspace_entry_point(gpu):
+    # largest first: every later call reads scratch bytes an earlier, bigger call wrote
+    cases = [("cfg3", None, 0), ("cfg2", 64, 0), ("cfg4", 16, 2048), ("cfg1_decode", None, 0), ("cfg2", 5, -1)]
+    for name, num_seqs, hint in cases:
+        print(f"[no_alloc] {name} num_seqs={num_seqs} hint={hint}", flush=True)
+        w = make_workload(name, gpu, num_seqs=num_seqs)
+        want = _with_workspace(w, hint)
+        got = _no_alloc(w, hint)
+        torch.cuda.synchronize()
+        assert bits_equal(got, want), f"{name} ({num_seqs} sequences)"
+        again = _no_alloc(w, hint)          # the same call again, on the scratch it left
+        torch.cuda.synchronize()
+        assert bits_equal(again, want), f"{name} ({num_seqs} sequences), second call"
+
