@@ -11,14 +11,15 @@
 // head g, so each K/V tile staged in LDS serves the whole GQA group. A work-group of eight
 // wavefronts (two per SIMD, one work-group per CU) owns the unit; wavefront w owns rows
 // 32 w .. 32 w + 31, which are 32 consecutive tokens of one head (TM >= 32 for every GQA
-// group built). The two wavefronts of a SIMD run the same loop out of phase, so one's
-// softmax overlaps the other's MFMAs.
+// group built). All eight wavefronts pass one barrier per K/V tile, so the two wavefronts
+// of a SIMD run the loop in step; what overlaps one's softmax with the other's MFMAs is
+// only the hardware's interleaving of their instructions.
 //
 // Three launches, all sized on the host without reading device memory:
 //   1. plan (one work-group): reads cu_seqlens_q/k, counts each unit's key tiles under
-//      its causal limit, picks a split size of max(8, total tiles / pool) tiles and writes
-//      the work list: every unit longer than the split size is cut into equal key ranges.
-//      Long items come first (a two-bucket longest-first order).
+//      its causal limit, picks a split size T = max(8, kSplitNum / kSplitDen x total tiles
+//      / pool) tiles and writes the work list: every unit longer than T is cut into equal
+//      key ranges. Long items come first (four length buckets, longest first).
 //   2. prefill (a persistent pool of one work-group per CU): each work-group claims items
 //      from the sub-queue of its XCD (item i belongs to sub-queue i mod 8, which for 8 kv
 //      heads is kv head i mod 8, so a head's K/V stays in one XCD's L2), then steals from
@@ -33,9 +34,10 @@
 //   online softmax down each column (a lane owns one query row; the two lane halves
 //   exchange through v_permlane32_swap)
 //   O^T (128 x 32)         += V^T (128 x 64) . P^T (64 x 32)   16 v_mfma_f32_32x32x16_bf16
-// K and V are staged row-major in a four-stage LDS ring (128 KiB) filled by DMA three tiles
-// ahead;
-// the P.V A operand comes from the LDS transpose read. P^T never leaves registers: the
+// K and V tiles move global -> registers -> LDS: two LDS stages of 16 KiB per operand
+// (sK[2], sV[2]); at step n the loads of tile n + 2 are issued, tile n is computed and
+// tile n + 1 is written from registers into the other stage. The P.V A operand comes
+// from the LDS transpose read. P^T never leaves registers: the
 // S^T accumulator layout already holds, per lane, the keys the P.V B operand needs once
 // the k-order of the instruction is permuted (same permutation on the V side).
 #include <algorithm>

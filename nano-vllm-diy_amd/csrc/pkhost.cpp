@@ -8,9 +8,11 @@
 //   src/engine/sequence.py:13-69        sequence state
 //   src/engine/model_runner.py:168-233  prepare_block_tables / prepare_seqs
 //   src/engine/llm_engine.py:70-105     add_request capacity checks
-// Prefix caching (block hashes, block_manager.py:96-181, 247-260) is not restated: a step
+// Prefix caching (block hashes, block_manager.py:96-181, 248-264) is not restated: a step
 // truncates a prefill sequence's cached count to a block boundary exactly as the
-// reference's hit-free prefix lookup does (block_manager.py:318), and never finds a hit.
+// reference's hit-free prefix lookup does (update_prefix_cache_block sets
+// num_cached_tokens = total_hits * block_size, block_manager.py:130-158, called at
+// scheduler.py:68-69), and never finds a hit.
 #include <cstdarg>
 #include <cstdio>
 #include <deque>

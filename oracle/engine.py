@@ -20,8 +20,8 @@ Restated (paths relative to the reference repository), in plain Python:
 Prefix caching is restated only as far as it acts when no block hash matches, which is
 every case where the cached blocks do not repeat a previous prompt's tokens: the lookup at
 the start of a prefill step sets num_cached_tokens to its block boundary
-(block_manager.py:266-318) and restores it when the sequence is not scheduled
-(:320-337).
+(update_prefix_cache_block, block_manager.py:130-158, called at scheduler.py:68-69) and
+restores it when the sequence is not scheduled (the undo closure, :160-177).
 
 Pinning (tests/test_host_engine.py): hand-worked schedules with closed-form arrays,
 invariants checked on every step of random workloads (token budget, sequence cap, block
