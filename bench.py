@@ -114,48 +114,112 @@ def sub_batch(w, keep):
     return q, cq, ck, bt, max(lq), max(lk)
 
 
-def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
-    """Oracle (CPU torch, all cores) on the first max_seqs sequences of w: store + attention."""
+def _host_sub_batch(w, ids):
+    """CPU copies of what the oracle needs for sequences `ids` of w: only the blocks they
+    read (renumbered), their query / new K / V rows, slots, lengths and block tables."""
+    import itertools
+    import math
+
+    import torch
+
+    bt = w.block_tables.cpu()
+    nblk = {b: math.ceil(w.k_lens[b] / 256) for b in ids}
+    blocks = sorted({int(x) for b in ids for x in bt[b, :nblk[b]].tolist()})
+    remap = {old: new for new, old in enumerate(blocks)}
+    idx = torch.tensor(blocks, dtype=torch.long, device=w.k_cache.device)
+    kc0 = w.k_cache.index_select(0, idx).cpu()
+    vc0 = w.v_cache.index_select(0, idx).cpu()
+    bt_sub = torch.full((len(ids), max(nblk.values())), -1, dtype=torch.int32)
+    for j, b in enumerate(ids):
+        bt_sub[j, :nblk[b]] = torch.tensor([remap[int(x)] for x in bt[b, :nblk[b]].tolist()], dtype=torch.int32)
+    cu = w.cu_seqlens_q.cpu().tolist()
+    rows = [r for b in ids for r in range(cu[b], cu[b + 1])]
+    ridx = torch.tensor(rows, dtype=torch.long, device=w.q.device)
+    slots = w.slot_mapping.cpu()[rows]
+    new_slots = torch.tensor([-1 if int(x) < 0 else remap[int(x) // 256] * 256 + int(x) % 256 for x in slots],
+                             dtype=torch.int32)
+    q, k, v = (t.index_select(0, ridx).cpu() for t in (w.q, w.k, w.v))
+    cu_q = torch.tensor([0, *itertools.accumulate(w.q_lens[b] for b in ids)], dtype=torch.int32)
+    cu_k = torch.tensor([0, *itertools.accumulate(w.k_lens[b] for b in ids)], dtype=torch.int32)
+    return q, k, v, kc0, vc0, new_slots, cu_q, cu_k, bt_sub
+
+
+def cpu_oracle_time(w, ids, reps: int = 3, store_only: bool = False) -> float:
+    """Median wall time (s) of the oracle (CPU torch, all host threads) running Attention.forward
+    on sequences `ids` of w: store of their new K/V rows, then paged attention."""
     import torch
 
     import oracle  # CPU baseline leg only
 
     torch.set_num_threads(os.cpu_count() or 1)
-    ids = list(range(min(max_seqs, len(w.q_lens))))
-    import math
-
-    bt = w.block_tables.cpu()
-    blocks = sorted({int(x) for b in ids for x in bt[b, :math.ceil(w.k_lens[b] / 256)].tolist()})
-    remap = {old: new for new, old in enumerate(blocks)}
-    idx = torch.tensor(blocks, dtype=torch.long, device=w.k_cache.device)
-    kc0 = w.k_cache.index_select(0, idx).cpu()
-    vc0 = w.v_cache.index_select(0, idx).cpu()
-    width = max(math.ceil(w.k_lens[b] / 256) for b in ids)
-    bt_sub = torch.full((len(ids), width), -1, dtype=torch.int32)
-    for j, b in enumerate(ids):
-        n = math.ceil(w.k_lens[b] / 256)
-        bt_sub[j, :n] = torch.tensor([remap[int(x)] for x in bt[b, :n].tolist()], dtype=torch.int32)
-    slots = w.slot_mapping.cpu()[ids]
-    new_slots = torch.tensor([remap[int(s) // 256] * 256 + int(s) % 256 for s in slots], dtype=torch.int32)
-    q = w.q[: len(ids)].cpu()
-    k = w.k[: len(ids)].cpu()
-    v = w.v[: len(ids)].cpu()
-    cu_q = torch.arange(len(ids) + 1, dtype=torch.int32)
-    cu_k = torch.tensor([0] + list(__import__("itertools").accumulate(w.k_lens[b] for b in ids)), dtype=torch.int32)
+    q, k, v, kc0, vc0, slots, cu_q, cu_k, bt = _host_sub_batch(w, ids)
     times = []
     for _ in range(reps):
         kc, vc = kc0.clone(), vc0.clone()
         t0 = time.perf_counter()
-        oracle.store_kvcache(k, v, kc, vc, new_slots)
-        oracle.varlen_attention(q, kc, vc, cu_q, cu_k, SCALE, True, bt_sub)
+        oracle.store_kvcache(k, v, kc, vc, slots)
+        if not store_only:
+            oracle.varlen_attention(q, kc, vc, cu_q, cu_k, SCALE, True, bt)
         times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baseline_decode(w, max_seqs: int, reps: int = 3):
+    """Oracle (CPU torch, all cores) on the first max_seqs sequences of w: store + attention."""
+    import torch
+
+    ids = list(range(min(max_seqs, len(w.q_lens))))
+    med = cpu_oracle_time(w, ids, reps)
     kv_bytes = sum(w.k_lens[b] * 2 * 2048 for b in ids)
-    med = statistics.median(times)
     return {"value": round(kv_bytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"CPU oracle (torch fp32 on {torch.get_num_threads()} threads, store + paged decode) "
                       f"on {len(ids)} of the 256 sequences ({kv_bytes / 1e9:.3f} GB of KV), "
                       f"median of {reps} runs = {med:.3f} s"}
+
+
+def cpu_baselines(dev, gpu_kernels: dict | None, reps: int = 3) -> dict:
+    """The oracle on the host cores for every other configuration, on the same seeded inputs
+    as the GPU measurements, each the full batch of its configuration (median of `reps`
+    runs): algorithmic GB/s (store, decode) or GFLOP/s (chunked prefill), and the GPU's
+    rate over the CPU's where the GPU figure was measured in this run."""
+    import torch
+
+    from pagedkv.workloads import make_workload
+
+    res = {"cores": torch.get_num_threads(), "kind": "port",
+           "what": "oracle/paged_kv.py (torch fp32) on all host threads: store of the new K/V rows, then "
+                   "paged attention, as Attention.forward; median of %d runs" % reps}
+    g = gpu_kernels or {}
+
+    def entry(name, sec, work, unit, gpu_key=None, gpu_field=None):
+        rate = work / sec / 1e9
+        e = {"s": round(sec, 4), unit: round(rate, 3)}
+        if gpu_key in g and gpu_field in g[gpu_key]:
+            e["gpu_over_cpu"] = round(g[gpu_key][gpu_field] / rate, 1)
+        res[name] = e
+
+    ws = make_workload("cfg1_store", dev)
+    entry("cfg1_store", cpu_oracle_time(ws, [0], reps, store_only=True), ws.store_bytes(), "GB/s",
+          "cfg1_store", "GB/s")
+    del ws
+    wd = make_workload("cfg1_decode", dev)
+    entry("cfg1_decode", cpu_oracle_time(wd, list(range(len(wd.q_lens))), reps), wd.decode_kv_bytes(), "GB/s",
+          "cfg1_forward_step", "GB/s")
+    del wd
+    w3 = make_workload("cfg3", dev)
+    dec = [i for i, lq in enumerate(w3.q_lens) if lq == 1]
+    pre = [i for i, lq in enumerate(w3.q_lens) if lq > 1]
+    entry("cfg3_decode", cpu_oracle_time(w3, dec, reps), w3.decode_kv_bytes(), "GB/s", "cfg3_decode", "GB/s")
+    entry("cfg3_prefill", cpu_oracle_time(w3, pre, reps), w3.prefill_flops(), "GFLOP/s", "cfg3_prefill", "TFLOP/s")
+    if "gpu_over_cpu" in res["cfg3_prefill"]:        # TFLOP/s over GFLOP/s
+        res["cfg3_prefill"]["gpu_over_cpu"] = round(res["cfg3_prefill"]["gpu_over_cpu"] * 1000, 1)
+    del w3
+    w4 = make_workload("cfg4", dev)
+    sec = cpu_oracle_time(w4, list(range(len(w4.q_lens))), reps)
+    entry("cfg4_decode", sec, w4.decode_kv_bytes(), "GB/s", "cfg4_decode", "logical_GB/s")
+    res["cfg4_decode"]["unique_GB/s"] = round(w4.decode_unique_kv_bytes() / sec / 1e9, 3)
+    return res
 
 
 def main() -> int:
@@ -287,6 +351,8 @@ def main() -> int:
         wc = make_workload("cfg2", dev)
         result["cpu_baseline"] = cpu_baseline_decode(wc, args.cpu_seqs)
         del wc
+        log("[bench] CPU baselines of the other configurations")
+        result["cpu_baselines"] = cpu_baselines(dev, result.get("kernels"))
     print(json.dumps(result), flush=True)
     return 0
 
@@ -296,12 +362,11 @@ def run_e2e(dev, seed: int = 5) -> dict:
     U[0, 151936), prompt and output lengths U[100, 1024], ignore_eos, greedy, block 256,
     16384-token budget. The timed region is generate() (requests added inside it, as in the
     reference's bench.py:67-72); model init and graph capture are outside."""
-    import random
-
     import torch
 
     from pagedkv.engine import LLMEngine
     from pagedkv.qwen3 import Qwen3Config
+    from pagedkv.workloads import serving_requests
 
     cfg = Qwen3Config()
     t0 = time.perf_counter()
@@ -309,10 +374,7 @@ def run_e2e(dev, seed: int = 5) -> dict:
                     max_num_batched_tokens=16384, seed=seed)
     torch.cuda.synchronize()
     init_s = time.perf_counter() - t0
-    rng = random.Random(seed)
-    prompts = [[rng.randrange(cfg.vocab_size) for _ in range(rng.randint(100, 1024))]
-               for _ in range(256)]
-    max_tokens = [rng.randint(100, 1024) for _ in range(256)]
+    prompts, max_tokens = serving_requests(seed, 256, cfg.vocab_size)
     outs, st = eng.generate(prompts, max_tokens, ignore_eos=True)
     assert [len(o) for o in outs] == max_tokens
     res = {"tok_per_s": round(st.tok_per_s, 1), "output_tokens": st.output_tokens,

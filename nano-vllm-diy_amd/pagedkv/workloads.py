@@ -257,3 +257,18 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
     seqs = [(1, prefix + x, bt) for x, bt in zip(suffixes, tables)]
     return _assemble(name, seqs, nb, seed * 1000 + 4, device, unique_blocks=nb,
                      meta={"shared_blocks": shared})
+
+
+def serving_requests(seed: int = 5, num_requests: int = 256, vocab_size: int = 151936,
+                     lo: int = 100, hi: int = 1024) -> tuple[list[list[int]], list[int]]:
+    """The offline serving workload: num_requests prompts of token ids uniform in
+    [0, vocab_size) with lengths uniform in [lo, hi], and output lengths uniform in [lo, hi]
+    (greedy, ignore_eos), drawn from random.Random(seed), prompts first and output lengths
+    after, in the order of the reference's bench.py:63-64 (which draws ids below 10000;
+    this workload draws them from the whole vocabulary)."""
+    import random
+
+    rng = random.Random(seed)
+    prompts = [[rng.randrange(vocab_size) for _ in range(rng.randint(lo, hi))] for _ in range(num_requests)]
+    max_tokens = [rng.randint(lo, hi) for _ in range(num_requests)]
+    return prompts, max_tokens

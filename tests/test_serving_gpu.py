@@ -1,0 +1,87 @@
+"""The serving configuration at its full size on the GPU: offline continuous batching of 256
+requests (seed 5: prompt ids uniform over the vocabulary, prompt and output lengths uniform
+in [100, 1024], greedy, ignore_eos) on the random-init 28-layer Qwen3-0.6B geometry, block
+size 256, 16384-token budget -- the workload bench.py times.
+
+Checks:
+  * every request gets exactly its max_tokens outputs and every block returns to the pool;
+  * three whole sequences, teacher-forced through the 28-layer CPU model oracle
+    (oracle/qwen3.py): a prompt long enough to be prefilled in two chunks, a request whose
+    1018 outputs span most of the run's decode steps, and the shortest request. Every
+    generated token's logit must lie within LOGIT_TOL of the oracle's maximum at its position,
+    and >= 90% of the tokens must be the oracle's argmax;
+  * graph vs eager: the same three requests on an eager engine (no HIP graphs, other batch
+    composition) are checked the same way, teacher-forced through the oracle. With random
+    weights the logits of a step lie close together, so the two runs part at the first
+    near-tie that bf16 rounding decides differently (both tokens within LOGIT_TOL of the
+    oracle's maximum there) and continue from different tokens after it.
+"""
+import pytest
+import torch
+
+import pagedkv.engine as E
+from oracle import qwen3 as Q
+from pagedkv.qwen3 import Qwen3Config
+from pagedkv.workloads import serving_requests
+from test_engine_gpu import LOGIT_TOL, _cpu_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _pick(prompts, max_tokens):
+    total = [len(p) + m for p, m in zip(prompts, max_tokens)]
+    short = [i for i in range(len(prompts)) if total[i] <= 1400]      # keeps the CPU oracle to seconds
+    chunked = max(short, key=lambda i: len(prompts[i]))
+    long_out = max(short, key=lambda i: max_tokens[i])
+    shortest = min(range(len(prompts)), key=lambda i: total[i])
+    return [chunked, long_out, shortest]
+
+
+def test_serving_workload_full_size(gpu):
+    cfg = Qwen3Config()
+    assert cfg.num_hidden_layers == 28
+    prompts, max_tokens = serving_requests(5, 256, cfg.vocab_size)
+    print("[serving] 256 requests, 28 layers: graph engine", flush=True)
+    eng = E.LLMEngine(cfg, device=gpu, num_blocks=2048, block_size=256, max_num_batched_tokens=16384, seed=5)
+    outs, stats = eng.generate(prompts, max_tokens, ignore_eos=True)
+    assert [len(o) for o in outs] == max_tokens
+    assert stats.output_tokens == sum(max_tokens) == 153791
+    assert stats.decode_steps > 0 and stats.prefill_steps > 0
+    assert eng.scheduler.num_free_blocks() == 2048
+    W = _cpu_weights(eng.runner.weights)
+    del eng
+    torch.cuda.empty_cache()
+
+    sel = _pick(prompts, max_tokens)
+    assert len(prompts[sel[0]]) > 512                                  # prefilled in two chunks
+    print(f"[serving] eager engine on requests {sel}", flush=True)
+    eager = E.LLMEngine(cfg, device=gpu, num_blocks=64, block_size=256, max_num_batched_tokens=16384, seed=5,
+                        enforce_eager=True)
+    outs_e, _ = eager.generate([prompts[i] for i in sel], [max_tokens[i] for i in sel], ignore_eos=True)
+    del eager
+    torch.cuda.empty_cache()
+
+    def teacher_forced(p, out, what):
+        """Every generated token within LOGIT_TOL of the oracle's max; returns argmax hits."""
+        logits = Q.forward_logits(W, cfg, p + out)
+        hits = 0
+        for t, tok in enumerate(out):
+            row = logits[len(p) - 1 + t]
+            best = float(row.max())
+            assert float(row[tok]) >= best - LOGIT_TOL, (what, t, tok, float(row[tok]), best)
+            hits += int(int(row.argmax()) == tok)
+        return hits
+
+    total = agree = 0
+    for j, i in enumerate(sel):
+        p, out, out_e = prompts[i], outs[i], outs_e[j]
+        assert len(out_e) == len(out)
+        diff = next((t for t in range(len(out)) if out[t] != out_e[t]), len(out))
+        print(f"[serving] oracle on request {i}: {len(p)} + {len(out)} tokens; graph and eager agree on the "
+              f"first {diff}", flush=True)
+        agree += teacher_forced(p, out, f"graph, request {i}")
+        total += len(out)
+        if diff < len(out):
+            agree += teacher_forced(p, out_e, f"eager, request {i}")
+            total += len(out_e)
+    assert agree >= 0.9 * total, f"{agree}/{total} tokens equal the oracle argmax"
