@@ -78,20 +78,23 @@ def timed_launches(fn, reps: int, warmup: int = 3, cold: bool = True):
     return statistics.fmean(ts), statistics.median(ts)
 
 
-def attention_call(w, sub=None):
-    """Closure running the path's attention op on workload w, or on a sub-batch of it."""
+def attention_call(w, sub=None, shared: bool = True):
+    """Closure running the path's attention op on workload w, or on a sub-batch of it, as
+    Attention.forward runs it: the batch's shared-prefix length from its block reference
+    counts (what an engine passes) is the cache hint and, when above 0, selects the
+    shared-prefix decode path (shared=False keeps the plain split-K path)."""
     import pagedkv
 
     q, cu_q, cu_k, bt, mq, mk = (w.q, w.cu_seqlens_q, w.cu_seqlens_k, w.block_tables,
                                  w.max_seqlen_q, w.max_seqlen_k) if sub is None else sub
-    # the batch's shared-prefix length from its block reference counts, as an engine passes it
     hint = w.shared_prefix_keys
+    sp = hint if shared and hint > 0 else None
     out = pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt,
-                                   cached_prefix_keys=hint)
+                                   cached_prefix_keys=hint, shared_prefix_keys=sp)
 
     def fn():
         pagedkv.varlen_attention(q, w.k_cache, w.v_cache, cu_q, cu_k, mq, mk, SCALE, True, bt, out=out,
-                                 cached_prefix_keys=hint)
+                                 cached_prefix_keys=hint, shared_prefix_keys=sp)
     return fn
 
 
@@ -530,7 +533,12 @@ def extra_configs(dev, w2):
     w4 = make_workload("cfg4", dev)
     ms, _ = timed_launches(attention_call(w4), 20)
     res["cfg4_decode"] = {"ms": round(ms, 5), "logical_GB/s": round(w4.decode_kv_bytes() / ms / 1e6, 1),
-                          "unique_GB/s": round(w4.decode_unique_kv_bytes() / ms / 1e6, 1)}
+                          "unique_GB/s": round(w4.decode_unique_kv_bytes() / ms / 1e6, 1),
+                          "path": "shared-prefix decode (the 8 shared blocks once, on MFMA) + split-K suffix"}
+    ms, _ = timed_launches(attention_call(w4, shared=False), 20)
+    res["cfg4_decode_plain"] = {"ms": round(ms, 5), "logical_GB/s": round(w4.decode_kv_bytes() / ms / 1e6, 1),
+                                "unique_GB/s": round(w4.decode_unique_kv_bytes() / ms / 1e6, 1),
+                                "path": "split-K over every key of every sequence"}
     return res
 
 

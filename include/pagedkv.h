@@ -155,6 +155,41 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride,
                            int32_t cached_prefix_keys, pk_stream_t stream);
 
 /*
+ * pk_varlen_attention_shared_prefix -- pk_varlen_attention_ex that computes the leading keys
+ * sequences share once per shared block instead of once per sequence (no counterpart in the
+ * reference, whose flash-attn call reads a shared prefix block again for every sequence that
+ * holds it, attention.py:95-104; prefix blocks are shared through the block manager's
+ * reference counts, block_manager.py:96-181).
+ *   shared_prefix_keys: the caller's bound on the shared prefix, e.g. the longest leading
+ *     run of blocks whose reference count exceeds 1 (pagedkv.shared_prefix_keys). For every
+ *     decode sequence (one query row) its keys below P = shared_prefix_keys, rounded down to
+ *     whole chunks of lcm(block_size, the decode split) keys, are processed in chunks: the
+ *     sequences whose block tables name the same blocks for a chunk (and hold the same number
+ *     of keys in it) put their query rows into one set of bf16 MFMA tiles, so each shared
+ *     block is read once; the keys past P go through the split-K decode kernel, and the
+ *     combine merges both. Sequences that share nothing are still correct (a group of one).
+ *     0 is pk_varlen_attention_ex. Paged mode only; prefill rows (Lq > 1) are unaffected.
+ *   Results: within the attention tolerance of pk_varlen_attention_ex (the prefix is summed
+ *   in another order), bit-identical from run to run, and bit-identical whether the prefix
+ *   blocks are shared or duplicated (a row's arithmetic does not depend on its tile mates).
+ *   Workspace: pk_varlen_attention_workspace_bytes, as for pk_varlen_attention_ex.
+ */
+int pk_varlen_attention_shared_prefix(const void* q, int64_t q_row_stride,
+                                      const void* k, const void* v,
+                                      int64_t k_row_stride, int64_t v_row_stride,
+                                      int64_t k_block_stride, int64_t v_block_stride,
+                                      const int32_t* block_table, int32_t block_table_stride,
+                                      int32_t block_size,
+                                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                      int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      float softmax_scale, int32_t causal,
+                                      void* out, int64_t out_row_stride,
+                                      void* workspace, size_t workspace_bytes,
+                                      int32_t cached_prefix_keys, int32_t shared_prefix_keys,
+                                      pk_stream_t stream);
+
+/*
  * pk_varlen_attention_noalloc -- pk_varlen_attention_ex for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. Same arguments, semantics and kernels as

@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
+#include <numeric>
 #include <string>
 
 #include "../../include/pagedkv.h"
@@ -50,11 +51,12 @@ struct WorkspaceLayout {
   // chunked-prefill plan region (only when max_seqlen_q > 1)
   int64_t pf_item_cap;
   size_t pf_queue_off, pf_items_off, pf_merges_off, pf_part_o_off, pf_part_ml_off;
+  size_t sp_plan_off;
   size_t total;
 };
 
-// [decode: per-split partial numerators | per-split (max, sum)]  (empty when no sequence
-// can have more than one split: those write their output directly)
+// [decode: per-split partial numerators | per-split (max, sum) | shared-prefix plan]  (empty
+// when no sequence can have more than one split: those write their output directly)
 // [prefill: queue header | work items | merge list | partial numerators | (max, sum)]
 WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_q, int max_seqlen_k) {
   WorkspaceLayout w{};
@@ -66,6 +68,10 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
     w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
   }
   size_t off = w.part_o_bytes + w.part_ml_bytes;
+  if (w.max_splits > 1) {  // the shared-prefix plan: at most one item per (sequence, slot)
+    w.sp_plan_off = off;
+    off += round_up(pk::shared_prefix_plan_bytes(num_seqs, w.max_splits), kWorkspaceAlign);
+  }
   if (max_seqlen_q > 1) {
     w.pf_item_cap = pk::prefill_item_cap(num_seqs, num_heads, max_seqlen_q);
     w.pf_queue_off = off;
@@ -134,7 +140,7 @@ int check_linear(const char* what, const void* x, int64_t x_row_stride, const vo
 
 extern "C" {
 
-int pk_abi_version(void) { return 8; }
+int pk_abi_version(void) { return 9; }
 
 const char* pk_last_error(void) { return g_last_error.c_str(); }
 
@@ -238,7 +244,7 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
                    int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
                    int32_t head_dim, float softmax_scale, int32_t causal, void* out, int64_t out_row_stride,
                    void* workspace, size_t workspace_bytes, int32_t cached_prefix_keys, const FusedProducer* fp,
-                   pk_stream_t stream) {
+                   int32_t shared_prefix_keys, pk_stream_t stream) {
   if (head_dim != pk::kHeadDim)
     return fail(PK_ERR_UNSUPPORTED, "varlen_attention: head_dim=%d not built (only %d)", head_dim, pk::kHeadDim);
   if (num_seqs < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
@@ -346,6 +352,26 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   }
   a.split_tokens = ws.split_tokens;
   a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
+  a.grid_splits = a.max_splits;
+  a.prefix_chunk = 1;
+  if (shared_prefix_keys > 0 && paged && !fp && ws.max_splits > 1 && num_seqs <= pk::kSharedPrefixMaxSeqs) {
+    // Shared-prefix decode. Chunks of CK = lcm(block_size, split) keys and a prefix of a
+    // whole number of chunks keep the partial slots within the workspace's: P / CK prefix
+    // slots + ceil((max_k - P) / split) split slots <= ceil(max_k / split).
+    const int s = ws.split_tokens;
+    const int ck = block_size / std::gcd(block_size, s) * s;
+    const int P = std::min(shared_prefix_keys, max_seqlen_k) / ck * ck;
+    if (P > 0 && ck / block_size <= pk::kSharedPrefixMaxChunkBlocks) {
+      a.prefix_keys = P;
+      a.prefix_chunk = ck;
+      a.prefix_slots = P / ck;
+      a.sp_plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ws.sp_plan_off);
+      a.grid_splits = (max_seqlen_k - P + s - 1) / s;
+      if (a.prefix_slots + a.grid_splits > a.max_splits)
+        return fail(PK_ERR_HIP, "varlen_attention: shared-prefix slots %d + %d exceed %d", a.prefix_slots,
+                    a.grid_splits, a.max_splits);
+    }
+  }
   char* const wsb = static_cast<char*>(workspace);
   if (ws.part_o_bytes > 0) {
     a.part_o = reinterpret_cast<float*>(wsb);
@@ -363,6 +389,10 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   }
 
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a.prefix_keys > 0) {
+    int rc = hip_status(pk::launch_shared_prefix(a, group, s), "shared-prefix launch");
+    if (rc != PK_OK) return rc;
+  }
   int rc = hip_status(pk::launch_decode(a, group, paged, max_seqlen_k, s), "decode launch");
   if (rc != PK_OK) return rc;
   if (max_seqlen_q > 1)
@@ -385,7 +415,28 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride, const void* k, c
   return attention_impl(q, q_row_stride, k, v, k_row_stride, v_row_stride, k_block_stride, v_block_stride,
                         block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs,
                         max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, causal, out,
-                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, nullptr, stream);
+                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, nullptr, 0, stream);
+}
+
+int pk_varlen_attention_shared_prefix(const void* q, int64_t q_row_stride, const void* k, const void* v,
+                                      int64_t k_row_stride, int64_t v_row_stride, int64_t k_block_stride,
+                                      int64_t v_block_stride, const int32_t* block_table,
+                                      int32_t block_table_stride, int32_t block_size,
+                                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                                      int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, float softmax_scale, int32_t causal,
+                                      void* out, int64_t out_row_stride, void* workspace, size_t workspace_bytes,
+                                      int32_t cached_prefix_keys, int32_t shared_prefix_keys, pk_stream_t stream) {
+  g_last_error.clear();
+  if (shared_prefix_keys < 0)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention_shared_prefix: shared_prefix_keys=%d < 0", shared_prefix_keys);
+  if (block_table == nullptr && shared_prefix_keys > 0)
+    return fail(PK_ERR_INVALID_ARG, "varlen_attention_shared_prefix: a shared prefix needs paged K/V (block_table)");
+  return attention_impl(q, q_row_stride, k, v, k_row_stride, v_row_stride, k_block_stride, v_block_stride,
+                        block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs,
+                        max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, causal, out,
+                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, nullptr, shared_prefix_keys,
+                        stream);
 }
 
 int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,
@@ -418,7 +469,7 @@ int pk_qkv_decode_attention(const void* qkv, int64_t qkv_row_stride, const int64
   return attention_impl(nullptr, 0, k_cache, v_cache, k_row_stride, v_row_stride, k_block_stride, v_block_stride,
                         block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs, 1,
                         max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, 1, out, out_row_stride,
-                        workspace, workspace_bytes, cached_prefix_keys, &fp, stream);
+                        workspace, workspace_bytes, cached_prefix_keys, &fp, 0, stream);
 }
 
 int pk_store_decode_attention(const void* q, int64_t q_row_stride, const void* key, int64_t key_row_stride,
@@ -447,7 +498,7 @@ int pk_store_decode_attention(const void* q, int64_t q_row_stride, const void* k
   return attention_impl(q, q_row_stride, k_cache, v_cache, k_row_stride, v_row_stride, k_block_stride,
                         v_block_stride, block_table, block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k,
                         num_seqs, 1, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, 1, out,
-                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, &fp, stream);
+                        out_row_stride, workspace, workspace_bytes, cached_prefix_keys, &fp, 0, stream);
 }
 
 int pk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, const int64_t* positions,
@@ -674,5 +725,5 @@ extern "C" int pk_varlen_attention_noalloc(const void* q, int64_t q_row_stride, 
   return attention_impl(q, q_row_stride, k, v, k_row_stride, v_row_stride, k_block_stride, v_block_stride, block_table,
                         block_table_stride, block_size, cu_seqlens_q, cu_seqlens_k, num_seqs, max_seqlen_q,
                         max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, causal, out, out_row_stride,
-                        ws, need > 0 ? (size_t)PK_NOALLOC_SCRATCH_BYTES : 0, cached_prefix_keys, nullptr, stream);
+                        ws, need > 0 ? (size_t)PK_NOALLOC_SCRATCH_BYTES : 0, cached_prefix_keys, nullptr, 0, stream);
 }

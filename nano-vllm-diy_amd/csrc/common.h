@@ -45,7 +45,20 @@ struct AttnArgs {
   int32_t stream_from;           // decode splits starting at key >= this use non-temporal loads (< 0: none)
   int32_t store_through;         // decode partials written through L2 (set by the decode launch)
   int32_t split_tokens;
-  int32_t max_splits;
+  int32_t max_splits;           // partial slots per sequence (stride of part_o / part_ml)
+  int32_t grid_splits;          // splits the decode grid covers per sequence
+  // Shared-prefix decode: keys [0, min(prefix_keys, Lk)) of a decode sequence are computed by
+  // the shared-prefix kernel, one partial per chunk of prefix_chunk keys in slots
+  // [0, prefix_slots); the split kernel covers the keys after them, its split s in slot
+  // prefix_slots + s. prefix_keys == 0 (prefix_chunk 1, prefix_slots 0): off.
+  int32_t prefix_keys;
+  int32_t prefix_chunk;
+  int32_t prefix_slots;
+  // Shared-prefix plan (workspace, after the decode partials): item counts per chunk
+  // (kSharedPrefixHeaderInts), then items [prefix_slots][num_seqs] of two int4 ((first member,
+  // members, keys held, 0), (block ids of the chunk)), then members [prefix_slots][num_seqs]
+  // int2 (sequence, query row) grouped by item.
+  int32_t* sp_plan;
   // chunked-prefill work plan (workspace): a work item is (sequence, kv head, query tile,
   // key-tile range); items of one query tile that was split over several key ranges write
   // fp32 partials that a merge pass combines.
@@ -81,6 +94,16 @@ struct AttnArgs {
   const uint16_t* new_v;
   int64_t new_v_stride;
 };
+
+// Shared-prefix decode limits: the plan groups sequences in one work-group (one thread per
+// sequence) and compares at most two block ids per chunk.
+constexpr int kSharedPrefixMaxSeqs = 1024;
+constexpr int kSharedPrefixMaxChunkBlocks = 2;
+constexpr int kSharedPrefixHeaderInts = 256;  // >= the partial slots of any launch
+// Plan bytes: header, items (2 int4) and members (int2) for num_seqs x slots chunks.
+inline size_t shared_prefix_plan_bytes(int num_seqs, int slots) {
+  return (size_t)kSharedPrefixHeaderInts * 4 + (size_t)num_seqs * slots * (32 + 8);
+}
 
 // Prefill plan sizes. The kernel runs kPrefillSlotsMax persistent work-groups at most (one
 // per CU on a 256-CU part). The split size T is at least 2/3 x total work / slots, and
@@ -146,6 +169,9 @@ hipError_t launch_gather_kv(const void* cache, int64_t block_stride, int32_t blo
 // Split-K decode over sequences with exactly one query row, plus the combine pass.
 hipError_t launch_decode(const AttnArgs& a, int group, bool paged, int max_seqlen_k,
                          hipStream_t stream);
+// Decode rows over their shared-prefix keys (a.prefix_keys > 0): MFMA tiles of the query rows
+// of every sequence whose block table names the same blocks, one partial per chunk.
+hipError_t launch_shared_prefix(const AttnArgs& a, int group, hipStream_t stream);
 // bf16-MFMA attention over sequences with more than one query row.
 hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal,
                           int max_seqlen_q, hipStream_t stream);

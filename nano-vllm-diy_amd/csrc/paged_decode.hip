@@ -338,11 +338,15 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
   const int k0 = a.cu_k[b], k1 = a.cu_k[b + 1];
   const int Lk = min(k1 - k0, a.max_seqlen_k);
-  const int t_begin = split * a.split_tokens;
+  // keys below Pb belong to the shared-prefix kernel (Pb = 0 when it is off)
+  const int Pb = max(0, min(a.prefix_keys, Lk));
+  const int t_begin = Pb + split * a.split_tokens;
   // rows with Lq != 1 belong to the prefill kernel; t_begin >= Lk also skips Lk <= 0 (graph padding)
   if ((q1 - q0 != 1) | (t_begin >= Lk)) return;
   const int t_end = min(Lk, t_begin + a.split_tokens);
-  const int nsplit = (Lk + a.split_tokens - 1) / a.split_tokens;
+  // partials of the sequence: its prefix chunks, then its splits
+  const int nsplit = (Pb + a.prefix_chunk - 1) / a.prefix_chunk + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
+  const int slot = a.prefix_slots + split;
 
   const int c = lane & 15;
   const int g_lane = g_first + (lane >> 4);               // this DPP row's kv head
@@ -401,7 +405,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   if (!row_live) return;
   // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous,
   // written through L2 or left in it by the launch's choice (kStoreThroughBytes).
-  const int64_t unit0 = ((int64_t)b * a.max_splits + split) * H;
+  const int64_t unit0 = ((int64_t)b * a.max_splits + slot) * H;
   const __amdgpu_buffer_rsrc_t po_rs = row_rsrc(a.part_o + unit0 * D, (uint32_t)(H * D * 4));
   const __amdgpu_buffer_rsrc_t pml_rs = row_rsrc(a.part_ml + unit0 * 2, (uint32_t)(H * 8));
 #pragma unroll
@@ -473,10 +477,15 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   if (q1 - q0 != 1) return;
   const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
   if (Lk <= 0) return;
-  const int nsplit = (Lk + a.split_tokens - 1) / a.split_tokens;
-  if (nsplit <= 1) return;  // written directly by the split kernel
+  // partial j < npre: prefix chunk j (slot j); the others: split j - npre (slot prefix_slots + j - npre)
+  const int Pb = min(a.prefix_keys, Lk);
+  const int npre = (Pb + a.prefix_chunk - 1) / a.prefix_chunk;
+  const int nsplit = npre + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
+  if (nsplit <= 1 && npre == 0) return;  // written directly by the split kernel
+  const int gap = a.prefix_slots - npre;
+  const auto slot_of = [&](int j) { return j < npre ? j : j + gap; };
   const int H = a.num_heads;
-  const int64_t unit0 = (int64_t)b * a.max_splits * H + h;  // partial of split j: unit0 + j H
+  const int64_t unit0 = (int64_t)b * a.max_splits * H + h;  // partial in slot j: unit0 + j H
   const int d = threadIdx.x;
   const float* po = a.part_o + unit0 * D + partial_slot(d);
   const int64_t stride = (int64_t)H * D;
@@ -486,10 +495,10 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
     // lanes 0 .. kCombineFast - 1 and broadcast by shuffles: no LDS, no barrier.
     const int lane = threadIdx.x & (kWave - 1);
     float2 ml = make_float2(-INFINITY, 0.f);
-    if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)lane * H) * 2);
+    if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)slot_of(lane) * H) * 2);
     float v[kCombineFast];
 #pragma unroll
-    for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[(int64_t)j * stride] : 0.f;
+    for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[(int64_t)slot_of(j) * stride] : 0.f;
     float mx = ml.x;
 #pragma unroll
     for (int m = kCombineFast / 2; m >= 1; m >>= 1) mx = fmaxf(mx, xor_shfl(mx, m));
@@ -507,11 +516,12 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   // Long contexts: split maxima and weights by block reductions into LDS, then thread d
   // forms the weighted sum of element d with four independent accumulators.
   float mx = -INFINITY;
-  for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) mx = fmaxf(mx, a.part_ml[(unit0 + (int64_t)j * H) * 2]);
+  for (int j = threadIdx.x; j < nsplit; j += kCombineThreads)
+    mx = fmaxf(mx, a.part_ml[(unit0 + (int64_t)slot_of(j) * H) * 2]);
   mx = block_reduce(mx, true, red);
   float lsum = 0.f;
   for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)j * H) * 2);
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)slot_of(j) * H) * 2);
     const float w = exp2_fast(ml.x - mx);
     w_s[j] = w;
     lsum = fmaf(w, ml.y, lsum);
@@ -520,12 +530,12 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
   int j = 0;
   for (; j + 4 <= nsplit; j += 4) {
-    o0 = fmaf(w_s[j], po[(int64_t)j * stride], o0);
-    o1 = fmaf(w_s[j + 1], po[(int64_t)(j + 1) * stride], o1);
-    o2 = fmaf(w_s[j + 2], po[(int64_t)(j + 2) * stride], o2);
-    o3 = fmaf(w_s[j + 3], po[(int64_t)(j + 3) * stride], o3);
+    o0 = fmaf(w_s[j], po[(int64_t)slot_of(j) * stride], o0);
+    o1 = fmaf(w_s[j + 1], po[(int64_t)slot_of(j + 1) * stride], o1);
+    o2 = fmaf(w_s[j + 2], po[(int64_t)slot_of(j + 2) * stride], o2);
+    o3 = fmaf(w_s[j + 3], po[(int64_t)slot_of(j + 3) * stride], o3);
   }
-  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], po[(int64_t)j * stride], o0);
+  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], po[(int64_t)slot_of(j) * stride], o0);
   a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(((o0 + o1) + (o2 + o3)) / lsum);
 }
 
@@ -536,7 +546,8 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
   while (quads % waves != 0) --waves;            // no idle wavefront in any work-group
   const int zgroups = quads / waves;
-  const dim3 grid((unsigned)(a.max_splits * a.num_seqs), (unsigned)zgroups);
+  if (a.grid_splits <= 0) return hipSuccess;  // every decode key lies in the shared prefix
+  const dim3 grid((unsigned)(a.grid_splits * a.num_seqs), (unsigned)zgroups);
   const dim3 block((unsigned)(waves * kWave));
   if (a.qkv != nullptr || a.new_k != nullptr)  // fused steps are paged only (checked by their entry points)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);

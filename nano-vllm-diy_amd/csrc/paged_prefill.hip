@@ -752,6 +752,250 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
   }
 }
 
+// ---- Shared-prefix decode ------------------------------------------------------------------
+// Decode rows (one query row per sequence) over keys [0, Pb), Pb = min(prefix_keys, Lk), in
+// chunks of prefix_chunk keys (one or two whole cache blocks). The sequences whose block
+// tables name the same blocks for a chunk, and that hold the same number of keys in it, form
+// a group -- with prefix caching, the sequences sharing those blocks. Work item = (chunk, up
+// to kPrefillRows / G members of a group); with kv head g it is one work unit: the members'
+// query rows (members x the G heads of g) form one MFMA tile set, so each shared block is
+// read once instead of once per sequence. Every row gets the chunk's (max, sum, numerator)
+// partial in the chunk's slot of its sequence, merged with the sequence's split partials by
+// the decode combine. A row's arithmetic does not depend on which other rows share its
+// tiles, so results do not depend on the grouping (shared or duplicated blocks give
+// identical bits) nor on the order in which the plan lists items.
+constexpr int kSpPlanThreads = kSharedPrefixMaxSeqs;
+
+// Exclusive prefix sum over the work-group (one value per thread) and the total.
+__device__ __forceinline__ int2 plan_scan(int v, int* s_w) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == kWave - 1) s_w[wave] = x;
+  __syncthreads();
+  int off = 0, tot = 0;
+  for (int w = 0; w < kSpPlanThreads / kWave; ++w) {
+    const int c = s_w[w];
+    off += w < wave ? c : 0;
+    tot += c;
+  }
+  __syncthreads();
+  return make_int2(off + x - v, tot);
+}
+
+// One work-group per chunk, thread b = sequence b. A sequence's chunk key is (keys held, first
+// block id, second block id); sequences with equal keys form a group, found through an LDS
+// hash table on the first block id (the first sequence to claim an entry leads the group).
+// Ranks inside a group come from an atomic counter, so the member order may change from run
+// to run -- which does not change any result (see above). Members are laid out group after
+// group; every member whose rank is a multiple of the item size starts an item.
+constexpr int kPlanHash = 2 * kSharedPrefixMaxSeqs;  // entries (more than sequences: probing ends)
+
+template <int G>
+__global__ __launch_bounds__(kSpPlanThreads) void prefix_plan_kernel(const AttnArgs a) {
+  constexpr int MC = kPrefillRows / G;
+  __shared__ int s_cnt[kSpPlanThreads], s_id0[kSpPlanThreads], s_id1[kSpPlanThreads], s_size[kSpPlanThreads],
+      s_base[kSpPlanThreads], s_tab[kPlanHash];
+  __shared__ int s_w[kSpPlanThreads / kWave];
+  __shared__ int s_items;
+  const int b = threadIdx.x;
+  const int c = blockIdx.x;
+  const int S = a.num_seqs;
+  const int BS = a.block_size;
+  const int CK = a.prefix_chunk;
+  const int Cb = CK / BS;
+  int cnt = 0, q0 = 0, id0 = -1, id1 = -1;
+  if (b < S) {
+    q0 = a.cu_q[b];
+    const int Lq = a.cu_q[b + 1] - q0;
+    const int Lk = min(a.cu_k[b + 1] - a.cu_k[b], a.max_seqlen_k);
+    if (Lq == 1) cnt = max(0, min(CK, min(a.prefix_keys, Lk) - c * CK));  // decode rows only
+    if (cnt > 0) {
+      const int32_t* bt = a.block_table + (int64_t)b * a.bt_stride + c * Cb;
+      id0 = bt[0];
+      if (Cb > 1 && cnt > BS) id1 = bt[1];
+    }
+  }
+  s_cnt[b] = cnt;
+  s_id0[b] = id0;
+  s_id1[b] = id1;
+  s_size[b] = 0;
+  for (int e = b; e < kPlanHash; e += kSpPlanThreads) s_tab[e] = -1;
+  if (b == 0) s_items = 0;
+  __syncthreads();
+  int lead = -1, rank = 0;
+  if (cnt > 0) {
+    int h = (int)(((uint32_t)id0 * 2654435761u) >> 21) & (kPlanHash - 1);
+    for (int probe = 0; probe < kPlanHash; ++probe, h = (h + 1) & (kPlanHash - 1)) {
+      const int e = atomicCAS(&s_tab[h], -1, b);
+      if (e == -1) {
+        lead = b;
+        break;
+      }
+      if (s_cnt[e] == cnt && s_id0[e] == id0 && s_id1[e] == id1) {
+        lead = e;
+        break;
+      }
+    }
+    if (lead >= 0) rank = atomicAdd(&s_size[lead], 1);
+  }
+  __syncthreads();
+  // s_size[x]: the size of the group x leads (0 if x leads none)
+  s_base[b] = plan_scan(s_size[b], s_w).x;  // the group's first position in the member list
+  __syncthreads();
+  int4* items = reinterpret_cast<int4*>(a.sp_plan + kSharedPrefixHeaderInts) + (int64_t)c * S * 2;
+  int2* members = reinterpret_cast<int2*>(a.sp_plan + kSharedPrefixHeaderInts + (int64_t)a.prefix_slots * S * 8) +
+                  (int64_t)c * S;
+  if (lead >= 0) {
+    const int pos = s_base[lead] + rank;
+    members[pos] = make_int2(b, q0);
+    if (rank % MC == 0) {
+      const int idx = atomicAdd(&s_items, 1);
+      items[2 * idx] = make_int4(pos, min(MC, s_size[lead] - rank), cnt, 0);
+      items[2 * idx + 1] = make_int4(id0, id1 >= 0 ? id1 : id0, 0, 0);
+    }
+  }
+  __syncthreads();
+  if (b == 0) a.sp_plan[c] = s_items;
+}
+
+template <int G>
+__global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_kernel(const AttnArgs a) {
+  static_assert(kRowBlocks == 1, "one 32-row block per wavefront");
+  constexpr int D = kHeadDim;
+  constexpr int MC = kPrefillRows / G;  // member sequences per item
+  __shared__ __attribute__((aligned(1024))) char sK[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sV[2][kTileBytes];
+  __shared__ int2 s_mem[MC];  // (sequence, query row)
+  lds_char* KS[2] = {(lds_char*)sK[0], (lds_char*)sK[1]};
+  lds_char* VS[2] = {(lds_char*)sV[0], (lds_char*)sV[1]};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int BS = a.block_size;
+  const int CK = a.prefix_chunk;
+  const int Cb = CK / BS;
+  const int S = a.num_seqs;
+  // grid (chunk, kv head, worker): work-groups go to the XCDs round-robin by linear id, so
+  // with the worker slowest the first (busiest) worker of every (chunk, head) spreads over
+  // all of them
+  const int c = blockIdx.x;
+  const int g = blockIdx.y;
+  const int4* items = reinterpret_cast<const int4*>(a.sp_plan + kSharedPrefixHeaderInts) + (int64_t)c * S * 2;
+  // this worker's first item is read together with the chunk's item count (the slot lies in
+  // the chunk's item list, blockIdx.z < num_seqs; it is used only if the count covers it)
+  int4 it = items[2 * blockIdx.z];
+  int4 ids = items[2 * blockIdx.z + 1];
+  const int n_items = min(a.sp_plan[c], S);
+  const int2* members =
+      reinterpret_cast<const int2*>(a.sp_plan + kSharedPrefixHeaderInts + (int64_t)a.prefix_slots * S * 8) +
+      (int64_t)c * S;
+  const TileLanes tl = tile_lanes(lane);
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  for (int i = blockIdx.z; i < n_items; i += gridDim.z) {
+    if (i != (int)blockIdx.z) {
+      it = items[2 * i];
+      ids = items[2 * i + 1];
+    }
+    const int nmem = min(it.y, MC);
+    const int cnt = it.z;
+    const int id0 = ids.x, id1 = ids.y;
+    // the plan is trusted only as far as the buffers reach (see prefill_item)
+    if (it.x < 0 || nmem <= 0 || it.x + nmem > S || cnt <= 0 || cnt > CK || (cnt > BS && Cb < 2)) continue;
+
+    // tile n: keys 64 n .. of the chunk, in its block (64 n) / BS; rows past cnt re-read the
+    // chunk's last key (same block) and are masked
+    const auto load = [&](int n, KvRegs& R) {
+      const int t0 = n * kTileKeys;
+      const int id = t0 < BS ? id0 : id1;
+      const int off = t0 % BS;
+      const uint16_t* kbase = a.k + (int64_t)id * a.k_block_stride + (int64_t)off * a.k_row_stride + g * D;
+      const uint16_t* vbase = a.v + (int64_t)id * a.v_block_stride + (int64_t)off * a.v_row_stride + g * D;
+      const LoadLanes l = load_lanes(a, wave, lane, min(kTileKeys, cnt - 1 - t0));
+#pragma unroll
+      for (int j = 0; j < kLoadsPerOperand; ++j) {
+        R.k[j] = *reinterpret_cast<const u32x4*>(kbase + l.k[j]);
+        R.v[j] = *reinterpret_cast<const u32x4*>(vbase + l.v[j]);
+      }
+    };
+    // the first two tiles are requested before the members and their q rows (which depend
+    // on the member list), so the three rounds of loads overlap
+    const int ntiles = (cnt + kTileKeys - 1) / kTileKeys;
+    KvRegs R0, R;
+    load(0, R0);
+    if (ntiles > 1) load(1, R);
+    __syncthreads();  // s_mem of the previous item has been read
+    if (tid < nmem) s_mem[tid] = members[it.x + tid];
+    __syncthreads();
+
+    // rows: 32 per wavefront; TMd = members rounded up to 32 rows per head, head i = row / TMd
+    const int TMd = (nmem + 31) & ~31;
+    const bool active = wave * 32 < G * TMd;
+    const int r0 = wave * 32;
+    const int hi = active ? r0 / TMd : 0;
+    const int mem = active ? r0 % TMd + col : 0;
+    const int2 sm = s_mem[min(mem, nmem - 1)];  // rows past the members read the last one's q
+    const int seq = min(max(sm.x, 0), a.num_seqs - 1);
+    const int h = g * G + hi;
+    bf16x8 qb[kRowBlocks][D / 16];
+    {
+      const uint16_t* qp = a.q + (int64_t)max(sm.y, 0) * a.q_row_stride + h * D + 8 * half;
+#pragma unroll
+      for (int kb = 0; kb < D / 16; ++kb)
+        qb[0][kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + kb * 16));
+    }
+    f32x16 o[kRowBlocks][4];
+    float m_i[kRowBlocks] = {-INFINITY}, l_i[kRowBlocks] = {0.f};
+    const int lim[kRowBlocks] = {cnt - 1};  // every member holds the chunk's cnt keys
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) o[0][md][rr] = 0.f;
+
+    store_tile_lds(R0, KS[0], VS[0], wave, lane);
+    lds_barrier();
+    for (int n0 = 0; n0 < ntiles; n0 += 2) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int n = n0 + st;
+        if (n >= ntiles) break;
+        const int t0 = n * kTileKeys;
+        KvRegs Rn;
+        if (n + 2 < ntiles) load(n + 2, Rn);
+        const bool full[kRowBlocks] = {t0 + kTileKeys - 1 <= lim[0]};
+        if (active) compute_tile(KS[st], VS[st], tl, qb, o, m_i, l_i, t0, lim, full, a.scale_log2, lane);
+        if (n + 1 < ntiles) store_tile_lds(R, KS[st ^ 1], VS[st ^ 1], wave, lane);
+        lds_barrier();
+        R = Rn;
+      }
+    }
+
+    // partial of (member, head h) in slot c, in the decode split kernel's layout: numerator
+    // element d at partial slot (d & 4 ? 64 : 0) + 4 (d >> 3) + (d & 3); O^T element rr of
+    // d-block md is d = 32 md + 8 (rr >> 2) + 4 half + (rr & 3), i.e. four consecutive slots
+    const float l_tot = swap_halves_sum(l_i[0]);
+    if (active && mem < nmem) {
+      const int64_t unit = ((int64_t)seq * a.max_splits + c) * a.num_heads + h;
+      float* po = a.part_o + unit * D + 64 * half;
+#pragma unroll
+      for (int md = 0; md < 4; ++md)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<float4*>(po + 16 * md + 4 * q) =
+              make_float4(o[0][md][4 * q], o[0][md][4 * q + 1], o[0][md][4 * q + 2], o[0][md][4 * q + 3]);
+      if (half == 0) *reinterpret_cast<float2*>(a.part_ml + unit * 2) = make_float2(m_i[0], l_tot);
+    }
+  }
+}
+
 int device_prefill_slots() {
   static int cached[64];
   int dev = 0;
@@ -785,6 +1029,33 @@ hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_
 }
 
 }  // namespace
+
+template <int G>
+void launch_shared_prefix_g(const AttnArgs& a, hipStream_t stream) {
+  // plan: one work-group per chunk; items: (chunk, kv head, worker), the workers of a chunk
+  // taking its items in turn, sized so the grid holds about two work-groups per CU
+  const int pool = 2 * device_prefill_slots();
+  const int workers = std::max(1, std::min(a.num_seqs, pool / std::max(1, a.prefix_slots * a.num_kv_heads)));
+  hipLaunchKernelGGL(prefix_plan_kernel<G>, dim3((unsigned)a.prefix_slots), dim3(kSpPlanThreads), 0, stream, a);
+  hipLaunchKernelGGL(shared_prefix_kernel<G>, dim3((unsigned)a.prefix_slots, (unsigned)a.num_kv_heads, (unsigned)workers),
+                     dim3(kPrefillThreads), 0, stream, a);
+}
+
+hipError_t launch_shared_prefix(const AttnArgs& a, int group, hipStream_t stream) {
+  if (a.num_seqs <= 0 || a.prefix_keys <= 0 || a.prefix_slots <= 0) return hipSuccess;
+  if (!a.block_table || !a.part_o || !a.part_ml || !a.sp_plan || a.num_seqs > kSharedPrefixMaxSeqs ||
+      a.prefix_chunk % a.block_size != 0 || a.prefix_chunk / a.block_size > kSharedPrefixMaxChunkBlocks ||
+      a.prefix_slots > kSharedPrefixHeaderInts)
+    return hipErrorInvalidValue;
+  switch (group) {
+    case 1: launch_shared_prefix_g<1>(a, stream); break;
+    case 2: launch_shared_prefix_g<2>(a, stream); break;
+    case 4: launch_shared_prefix_g<4>(a, stream); break;
+    case 8: launch_shared_prefix_g<8>(a, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal, int max_seqlen_q,
                           hipStream_t stream) {

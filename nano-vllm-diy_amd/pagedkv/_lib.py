@@ -47,6 +47,12 @@ SIGNATURES = {
         _i32, _i32, _i32, ctypes.c_float, _i32, _c_void_p, _i64, _c_void_p, _size_t,
         _i32,                               # cached_prefix_keys
         _c_void_p]),                        # stream
+    "pk_varlen_attention_shared_prefix": (ctypes.c_int, [
+        _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+        _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
+        _i32, _i32, _i32, ctypes.c_float, _i32, _c_void_p, _i64, _c_void_p, _size_t,
+        _i32, _i32,                         # cached_prefix_keys, shared_prefix_keys
+        _c_void_p]),                        # stream
     "pk_varlen_attention_noalloc": (ctypes.c_int, [
         _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
         _c_void_p, _i32, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
@@ -115,7 +121,7 @@ SIGNATURES = {
         _c_void_p, _size_t, _c_void_p]),    # workspace, workspace_bytes, stream
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -19,7 +19,10 @@ every device operation is a hand-written gfx950 HIP kernel from libpagedkv.so:
   block no other sequence reads. With prefix caching that can fail: a fully cached prompt
   recomputes its last token (scheduler.py:77-80, model_runner.py:185-186) into a block
   other live sequences share. The reference's eight-field Context carries no such
-  statement, so it always gets the two launches, whose store is ordered before every read.
+  statement, so it always gets the two launches, whose store is ordered before every read;
+* a Context stating a shared prefix (ctx.cached_prefix_keys > 0) also selects the
+  shared-prefix decode path: the decode rows' keys below it are computed once per shared
+  block for all sequences that hold it (pk_varlen_attention_shared_prefix).
 
 The runner rebinds k_cache / v_cache to per-layer views of its KV tensor
 (model_runner.py:159-165), exactly as with the reference layer.
@@ -71,8 +74,10 @@ class Attention(nn.Module):
                                           cached_prefix_keys=hint)
         if bound:
             store_kvcache(k, v, k_cache, v_cache, ctx.slot_mapping)
+        shared = None
         if ctx.block_tables is not None:
             k, v = k_cache, v_cache
+            shared = hint if hint is not None and hint > 0 else None
         return varlen_attention(
             q, k, v,
             cu_seqlens_q=ctx.cu_seqlens_q,
@@ -83,4 +88,5 @@ class Attention(nn.Module):
             causal=True,
             block_table=ctx.block_tables,
             cached_prefix_keys=hint,
+            shared_prefix_keys=shared,
         )

@@ -8,9 +8,12 @@ Context (src/utils/context.py:5-14), built by the runner (model_runner.py:174-23
 * context_lens: (S,) int32 key length per sequence; produced by the runner and,
   as in the reference, not read by Attention.
 * block_tables: (S, W) int32, -1 padded; None selects flat (fresh K/V) attention.
-* cached_prefix_keys (an addition; results never depend on it): the decode cache hint,
-  the longest prefix the batch's sequences share (shared_prefix_keys); None keeps the
-  library default.
+* cached_prefix_keys (an addition): the longest prefix the batch's sequences share
+  (shared_prefix_keys), in keys. Decode reads past it stream (a cache hint); above 0 it also
+  selects the shared-prefix decode path, which computes the shared blocks once for all the
+  sequences that hold them (results within the attention tolerance of the plain path).
+  0 states that no block is shared (and allows the one-launch store + decode); None keeps
+  the library default.
 """
 from __future__ import annotations
 

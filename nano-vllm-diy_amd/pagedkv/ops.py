@@ -132,7 +132,8 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      block_table: torch.Tensor | None = None,
                      out: torch.Tensor | None = None,
                      cached_prefix_keys: int | None = None,
-                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+                     workspace: torch.Tensor | None = None,
+                     shared_prefix_keys: int | None = None) -> torch.Tensor:
     """Causal varlen attention with optional paged K/V; bf16 in and out.
 
     Same arguments and meaning as the flash_attn_varlen_func call of the reference
@@ -148,6 +149,10 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     read). None keeps the library default (PK_CACHED_PREFIX_KEYS_DEFAULT = 2048).
     workspace: caller-owned uint8 scratch of at least workspace_bytes(...) bytes (as the
     C-ABI takes it); None takes one per call (or the reserved one under graph capture).
+    shared_prefix_keys (an addition, paged mode): decode keys below it are computed once per
+    shared cache block, the query rows of every sequence that holds the block in one MFMA
+    tile (pk_varlen_attention_shared_prefix); results stay within the attention tolerance.
+    None or 0: off.
     """
     nq, num_heads, head_dim = q.shape
     dev = q.device
@@ -206,7 +211,11 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             scale, 1 if causal else 0,
             out.data_ptr(), out.stride(0),
             ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0)
-    if cached_prefix_keys is None:
+    if shared_prefix_keys and block_table is not None:
+        hint = PK_CACHED_PREFIX_KEYS_DEFAULT if cached_prefix_keys is None else int(cached_prefix_keys)
+        check(lib().pk_varlen_attention_shared_prefix(*args, hint, int(shared_prefix_keys), _stream(q)),
+              "pk_varlen_attention_shared_prefix")
+    elif cached_prefix_keys is None:
         check(lib().pk_varlen_attention(*args, _stream(q)), "pk_varlen_attention")
     else:
         check(lib().pk_varlen_attention_ex(*args, int(cached_prefix_keys), _stream(q)), "pk_varlen_attention_ex")

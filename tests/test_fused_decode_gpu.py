@@ -165,9 +165,13 @@ class _Spy:
 
 
 def _two_launches(q, key, value, kc, vc, ctx, scale):
+    """store_kvcache + varlen_attention as Attention.forward calls them (a stated shared
+    prefix also selects the shared-prefix decode path)."""
+    hint = ctx.cached_prefix_keys
     pagedkv.store_kvcache(key, value, kc, vc, ctx.slot_mapping)
     return pagedkv.varlen_attention(q, kc, vc, ctx.cu_seqlens_q, ctx.cu_seqlens_k, 1, ctx.max_seqlen_k, scale, True,
-                                    ctx.block_tables, cached_prefix_keys=ctx.cached_prefix_keys)
+                                    ctx.block_tables, cached_prefix_keys=hint,
+                                    shared_prefix_keys=hint if hint is not None and hint > 0 else None)
 
 
 def test_shared_token_block_takes_two_launches(gpu, monkeypatch):

@@ -81,6 +81,9 @@ def test_workspace_size_formula():
     split = 512
     units = 256 * (8192 // split) * HQ
     want = math.ceil(units * HEAD_DIM * 4 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
+    # + the shared-prefix plan: item counts per chunk (1 KiB), then per (sequence, slot) one
+    # item (32 B) and one member (8 B)
+    want += math.ceil((1024 + 256 * (8192 // split) * 40) / 256) * 256
     assert ws == want
 
 
@@ -358,3 +361,23 @@ def test_no_alloc_refuses_bounds_beyond_its_scratch():
     # nothing to do: success without touching the device
     assert lib.pk_varlen_attention_noalloc(None, HQ * HEAD_DIM, None, None, row, row, 0, 0, None, 0, 0, None, None,
                                            0, 1, 1, HQ, HKV, HEAD_DIM, 0.088, 1, None, HQ * HEAD_DIM, 0, None) == 0
+
+
+def test_shared_prefix_argument_checks():
+    """pk_varlen_attention_shared_prefix refuses a negative bound and a shared prefix in flat
+    mode (no block tables to share blocks through) before any launch; 0 sequences is a no-op."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x10000)
+    row = HKV * HEAD_DIM
+    base = [fake, HQ * HEAD_DIM, fake, fake, row, row, BLOCK_SIZE * row, BLOCK_SIZE * row, fake, 32, BLOCK_SIZE,
+            fake, fake, 4, 1, 4096, HQ, HKV, HEAD_DIM, 0.088, 1, fake, HQ * HEAD_DIM, None, 0, 2048]
+    assert lib.pk_varlen_attention_shared_prefix(*base, -1, None) == _lib.PK_ERR_INVALID_ARG
+    flat = list(base)
+    flat[8] = None
+    assert lib.pk_varlen_attention_shared_prefix(*flat, 512, None) == _lib.PK_ERR_INVALID_ARG
+    assert b"paged" in lib.pk_last_error()
+    # a workspace is still required (decode partials): refused before any launch
+    assert lib.pk_varlen_attention_shared_prefix(*base, 512, None) == _lib.PK_ERR_WORKSPACE
+    empty = list(base)
+    empty[13] = 0
+    assert lib.pk_varlen_attention_shared_prefix(*empty, 512, None) == _lib.PK_OK

@@ -448,7 +448,8 @@ def test_cache_hint_never_changes_results(gpu, name, num_seqs):
 
 def test_attention_forward_accepts_reference_context(gpu):
     """The layer takes the reference's eight-field Context (no cache hint) and gives the
-    same output as with this package's Context."""
+    same output as with this package's Context when that states no shared prefix either
+    (a stated prefix selects the shared-prefix decode path, tested on its own)."""
     import dataclasses
 
     @dataclasses.dataclass
@@ -463,7 +464,7 @@ def test_attention_forward_accepts_reference_context(gpu):
         block_tables: torch.Tensor | None = None
 
     w = make_workload("cfg4", gpu)
-    c = w.ctx
+    c = dataclasses.replace(w.ctx, cached_prefix_keys=None)
     ref_ctx = RefContext(c.is_prefill, c.cu_seqlens_q, c.cu_seqlens_k, c.max_seqlen_q, c.max_seqlen_k,
                          c.slot_mapping, c.context_lens, c.block_tables)
     kc0, vc0 = w.k_cache.clone(), w.v_cache.clone()
