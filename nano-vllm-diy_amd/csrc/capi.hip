@@ -81,7 +81,7 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
     w.pf_merges_off = off;
     off += round_up((size_t)pk::kPrefillMergeCap * 16, kWorkspaceAlign);
     w.pf_part_o_off = off;
-    off += (size_t)pk::kPrefillPartCap * 32 * pk::kPrefillRows * 4 * sizeof(float);
+    off += (size_t)pk::kPrefillPartCap * 32 * pk::kPrefillRows * 4 * sizeof(uint16_t);
     w.pf_part_ml_off = off;
     off += round_up((size_t)pk::kPrefillPartCap * pk::kPrefillRows * 2 * sizeof(float), kWorkspaceAlign);
   }
@@ -381,7 +381,7 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
     a.pf_queue = reinterpret_cast<int32_t*>(wsb + ws.pf_queue_off);
     a.pf_items = reinterpret_cast<int4*>(wsb + ws.pf_items_off);
     a.pf_merges = reinterpret_cast<int4*>(wsb + ws.pf_merges_off);
-    a.pf_part_o = reinterpret_cast<float*>(wsb + ws.pf_part_o_off);
+    a.pf_part_o = reinterpret_cast<uint16_t*>(wsb + ws.pf_part_o_off);
     a.pf_part_ml = reinterpret_cast<float*>(wsb + ws.pf_part_ml_off);
     a.pf_item_cap = (int32_t)std::min<int64_t>(ws.pf_item_cap, INT32_MAX);
     a.pf_merge_cap = pk::kPrefillMergeCap;

@@ -66,7 +66,7 @@ struct AttnArgs {
   int4* pf_items;               // [pf_item_cap] groups (b, qt, tile_begin | tile_end << 16, partial group);
                                 // item i = kv head i % Hkv of group i / Hkv
   int4* pf_merges;              // [pf_merge_cap] split units (b, qt, first partial group, splits)
-  float* pf_part_o;             // [part][32 chunks of 4 dims][kPrefillRows][4] unnormalised numerators
+  uint16_t* pf_part_o;          // [part][32 chunks of 4 dims][kPrefillRows][4] the split's output (bf16)
   float* pf_part_ml;            // [part][kPrefillRows][2] = (running max in the exp2 domain, sum)
   int32_t pf_item_cap;
   int32_t pf_merge_cap;

@@ -72,6 +72,10 @@ constexpr int kSplitDen = PK_PREFILL_SPLIT_DEN;
 constexpr int kMergeThreads = 256;     // merge: thread = row of the unit
 constexpr int kMergeGroups = 1024;
 constexpr int kMergeBatch = 8;         // merge: splits whose (max, sum) load in one batch
+#ifndef PK_MERGE_LOADS
+#define PK_MERGE_LOADS 4
+#endif
+constexpr int kMergeLoads = PK_MERGE_LOADS;  // merge: splits whose outputs load in one batch
 constexpr int kBuckets = 4;            // length buckets of the work list (longest first)
 constexpr float kLazyLog2 = 8.f;       // reference max moves only when exceeded by 2^8
 
@@ -285,7 +289,10 @@ __device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char*
       for (int rr = 0; rr < 16; ++rr) s[rb][mb][rr] = 0.f;
   // K A operand of half-tile mb, k-block kb, read in batches of kKBatch k-blocks (both
   // half-tiles) ahead of their MFMAs.
-  constexpr int kKBatch = kRowBlocks == 1 ? kHeadDim / 16 : kHeadDim / 32;
+#ifndef PK_PREFILL_KBATCH
+#define PK_PREFILL_KBATCH (kRowBlocks == 1 ? kHeadDim / 16 : kHeadDim / 32)
+#endif
+  constexpr int kKBatch = PK_PREFILL_KBATCH;
 #pragma unroll
   for (int k0b = 0; k0b < kHeadDim / 16; k0b += kKBatch) {
     bf16x8 ka[2][kKBatch];
@@ -592,17 +599,20 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
           *reinterpret_cast<uint2*>(op + md * 32 + 8 * gq) = w;
         }
     } else if (part < a.pf_part_cap) {
-      // numerators chunk-major (chunk = 4 dims = d / 4), so one store instruction writes two
-      // contiguous 512-byte runs (32 rows x 16 bytes per lane half)
-      float* po = a.pf_part_o + (int64_t)part * (32 * kPrefillRows * 4);
+      // The split's own output o / l in bf16 -- as precise as an unsplit row's output -- with
+      // (max, sum) in fp32 for the merge. Chunk-major (chunk = 4 dims = d / 4): one store
+      // instruction writes two contiguous 256-byte runs (32 rows x 8 bytes per lane half).
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      uint16_t* po = a.pf_part_o + (int64_t)part * (32 * kPrefillRows * 4);
 #pragma unroll
       for (int md = 0; md < 4; ++md)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const int chunk = 8 * md + 2 * gq + half;
-          const float4 w = make_float4(o[rb][md][4 * gq], o[rb][md][4 * gq + 1], o[rb][md][4 * gq + 2],
-                                       o[rb][md][4 * gq + 3]);
-          *reinterpret_cast<float4*>(po + ((int64_t)chunk * kPrefillRows + row[rb]) * 4) = w;
+          uint2 w;
+          w.x = pack_bf16x2(o[rb][md][4 * gq] * inv, o[rb][md][4 * gq + 1] * inv);
+          w.y = pack_bf16x2(o[rb][md][4 * gq + 2] * inv, o[rb][md][4 * gq + 3] * inv);
+          *reinterpret_cast<uint2*>(po + ((int64_t)chunk * kPrefillRows + row[rb]) * 4) = w;
         }
       if (half == 0)
         *reinterpret_cast<float2*>(a.pf_part_ml + ((int64_t)part * kPrefillRows + row[rb]) * 2) =
@@ -659,11 +669,11 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel
   }
 }
 
-// Merge the partials of every split unit: out = sum_s w_s o_s / sum_s w_s l_s with
-// w_s = exp2(m_s - max_s m_s). Work item = (split unit, quarter of head_dim, kv head);
-// thread t owns row t of the unit and 8 chunks of 4 dims.
-// At most 4 wavefronts per SIMD: the register budget lets all of a split's loads be in
-// flight at once instead of one 16-byte load per memory latency.
+// Merge the partials of every split unit: out = sum_s w_s o_s / sum_s w_s with
+// w_s = exp2(m_s - max_s m_s) l_s, o_s the split's normalised output (bf16). Work item =
+// (split unit, quarter of head_dim, kv head); thread t owns row t of the unit and 8 chunks
+// of 4 dims. At most 4 wavefronts per SIMD: the register budget lets the loads of
+// kMergeLoads splits be in flight at once.
 template <int G>
 __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void prefill_merge_kernel(
     const AttnArgs a) {
@@ -693,14 +703,19 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
     const int h = g * G + r / TM;
     if (tok >= Lq) continue;
     if ((int64_t)(pg + n) * hkv > a.pf_part_cap) continue;  // the plan bounds partial ids
-    // (max, sum) of the first kMergeBatch splits in one batch of loads; then the numerators,
-    // the loads of split s + 1 in flight while split s is accumulated
+    // Every load below reads a valid split (index clamped to the last one) and a split past
+    // the end gets weight 0: no load sits behind a branch, so the compiler's wait counts see
+    // a whole batch in flight instead of waiting out each load in turn.
+    const int last = n - 1;
     const float* ml_base = a.pf_part_ml + ((int64_t)(pg * hkv + g) * kPrefillRows + r) * 2;
     const int64_t ml_step = (int64_t)hkv * kPrefillRows * 2;  // next split of the unit
+    const auto load_ml = [&](int s2) {
+      const float2 v = *reinterpret_cast<const float2*>(ml_base + min(s2, last) * ml_step);
+      return s2 < n ? v : make_float2(-INFINITY, 0.f);
+    };
     float2 ml[kMergeBatch];
 #pragma unroll
-    for (int s2 = 0; s2 < kMergeBatch; ++s2)
-      ml[s2] = s2 < n ? *reinterpret_cast<const float2*>(ml_base + s2 * ml_step) : make_float2(-INFINITY, 0.f);
+    for (int s2 = 0; s2 < kMergeBatch; ++s2) ml[s2] = load_ml(s2);
     float M = -INFINITY;
 #pragma unroll
     for (int s2 = 0; s2 < kMergeBatch; ++s2) M = fmaxf(M, ml[s2].x);
@@ -711,33 +726,34 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
     float L = 0.f;
     if (M != -INFINITY) {
       const int64_t po_step = (int64_t)hkv * (32 * kPrefillRows * 4);
-      const float* po_base = a.pf_part_o + (int64_t)(pg * hkv + g) * (32 * kPrefillRows * 4) +
-                             ((int64_t)c0 * kPrefillRows + r) * 4;
-      const auto load = [&](int s2, f32x4 (&v)[CQ]) {
+      const uint16_t* po_base = a.pf_part_o + (int64_t)(pg * hkv + g) * (32 * kPrefillRows * 4) +
+                                ((int64_t)c0 * kPrefillRows + r) * 4;
+      const auto load = [&](int s2, uint2 (&v)[CQ]) {
 #pragma unroll
         for (int c = 0; c < CQ; ++c)
-          v[c] = *reinterpret_cast<const f32x4*>(po_base + s2 * po_step + (int64_t)c * kPrefillRows * 4);
+          v[c] = *reinterpret_cast<const uint2*>(po_base + min(s2, last) * po_step + (int64_t)c * kPrefillRows * 4);
       };
-      const auto add = [&](int s2, const f32x4 (&v)[CQ]) {
-        const float2 m = s2 < kMergeBatch ? ml[s2] : *reinterpret_cast<const float2*>(ml_base + s2 * ml_step);
-        const float wgt = exp2_fast(m.x - M);  // 0 for a split whose rows saw no key
-        L += wgt * m.y;
+      const auto add = [&](float2 m, const uint2 (&v)[CQ]) {
+        const float wgt = exp2_fast(m.x - M) * m.y;  // 0 for a split past the end or that saw no key
+        L += wgt;
 #pragma unroll
         for (int c = 0; c < CQ; ++c) {
-          acc[c].x += wgt * v[c][0];
-          acc[c].y += wgt * v[c][1];
-          acc[c].z += wgt * v[c][2];
-          acc[c].w += wgt * v[c][3];
+          acc[c].x += wgt * bf16_lo(v[c].x);
+          acc[c].y += wgt * bf16_hi(v[c].x);
+          acc[c].z += wgt * bf16_lo(v[c].y);
+          acc[c].w += wgt * bf16_hi(v[c].y);
         }
       };
-      f32x4 va[CQ], vb[CQ];
-      load(0, va);
-      for (int s2 = 0; s2 < n; s2 += 2) {
-        if (s2 + 1 < n) load(s2 + 1, vb);
-        add(s2, va);
-        if (s2 + 1 >= n) break;
-        if (s2 + 2 < n) load(s2 + 2, va);
-        add(s2 + 1, vb);
+      uint2 v[kMergeLoads][CQ];
+#pragma unroll
+      for (int j = 0; j < kMergeLoads; ++j) load(j, v[j]);
+#pragma unroll
+      for (int j = 0; j < kMergeLoads; ++j) add(ml[j], v[j]);
+      for (int s0 = kMergeLoads; s0 < n; s0 += kMergeLoads) {  // units of many splits
+#pragma unroll
+        for (int j = 0; j < kMergeLoads; ++j) load(s0 + j, v[j]);
+#pragma unroll
+        for (int j = 0; j < kMergeLoads; ++j) add(load_ml(s0 + j), v[j]);
       }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
