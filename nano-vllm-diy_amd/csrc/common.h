@@ -62,7 +62,7 @@ struct AttnArgs {
   // chunked-prefill work plan (workspace): a work item is (sequence, kv head, query tile,
   // key-tile range); items of one query tile that was split over several key ranges write
   // fp32 partials that a merge pass combines.
-  int32_t* pf_queue;            // kPrefillQueueInts header: 8 claim counters, item / merge counts
+  int32_t* pf_queue;            // kPrefillQueueInts header: 8 claim counters, item / merge counts, split size
   int4* pf_items;               // [pf_item_cap] groups (b, qt, tile_begin | tile_end << 16, partial group);
                                 // item i = kv head i % Hkv of group i / Hkv
   int4* pf_merges;              // [pf_merge_cap] split units (b, qt, first partial group, splits)
@@ -110,7 +110,9 @@ inline size_t shared_prefix_plan_bytes(int num_seqs, int slots) {
 // every split unit has more than T tiles, so its n splits satisfy n < 2 t / T: fewer than
 // 3 x slots partials (all kv heads) ever exist, in fewer than 1.5 x slots split units.
 constexpr int kPrefillSlotsMax = 256;
-constexpr int kPrefillQueueInts = 64;   // header ints (256 bytes)
+constexpr int kPrefillQueueStride = 32;  // claim counter q at pf_queue[32 q]: one 128-byte line each
+constexpr int kPrefillQueueMeta = 8 * kPrefillQueueStride;  // then item count, merge count, split size
+constexpr int kPrefillQueueInts = kPrefillQueueMeta + 64;   // header ints (1280 bytes)
 constexpr int kPrefillRows = 256;       // query rows per work item (query tokens x GQA heads)
 constexpr int kPrefillPartCap = 3 * kPrefillSlotsMax;
 constexpr int kPrefillMergeCap = 3 * kPrefillSlotsMax / 2;

@@ -76,7 +76,10 @@ constexpr int kMergeBatch = 8;         // merge: splits whose (max, sum) load in
 #define PK_MERGE_LOADS 4
 #endif
 constexpr int kMergeLoads = PK_MERGE_LOADS;  // merge: splits whose outputs load in one batch
-constexpr int kBuckets = 4;            // length buckets of the work list (longest first)
+#ifndef PK_PREFILL_BUCKETS
+#define PK_PREFILL_BUCKETS 4
+#endif
+constexpr int kBuckets = PK_PREFILL_BUCKETS;  // length buckets of the work list (longest first)
 constexpr float kLazyLog2 = 8.f;       // reference max moves only when exceeded by 2^8
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -369,7 +372,8 @@ __device__ __forceinline__ int split_begin(int t, int n, int s) { return (int)((
 
 // Length bucket of a group of t tiles (0 = longest) for split size T.
 __device__ __forceinline__ int length_bucket(int t, int T) {
-  return t * kBuckets > (kBuckets - 1) * T ? 0 : t * kBuckets > (kBuckets - 2) * T ? 1 : t * kBuckets > T ? 2 : 3;
+  const int j = (int)min((int64_t)kBuckets - 1, ((int64_t)t * kBuckets + T - 1) / T - 1);  // ceil(t K / T) - 1
+  return kBuckets - 1 - max(0, j);
 }
 
 // Work list. Waves take sequences in turn and lanes take a sequence's query tiles, so a
@@ -471,19 +475,22 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const AttnAr
     }
   }
   __syncthreads();
-  if (tid < 8) a.pf_queue[tid] = 0;
+  if (tid < 8) a.pf_queue[tid * kPrefillQueueStride] = 0;
   if (tid == 0) {
-    a.pf_queue[8] = (int)(min((int64_t)tot, (int64_t)a.pf_item_cap) * hkv);
-    a.pf_queue[9] = (int)(min((int64_t)cur[kBuckets + 1], (int64_t)a.pf_merge_cap) * hkv);
-    a.pf_queue[10] = T;
+    a.pf_queue[kPrefillQueueMeta] = (int)(min((int64_t)tot, (int64_t)a.pf_item_cap) * hkv);
+    a.pf_queue[kPrefillQueueMeta + 1] = (int)(min((int64_t)cur[kBuckets + 1], (int64_t)a.pf_merge_cap) * hkv);
+    a.pf_queue[kPrefillQueueMeta + 2] = T;
   }
 }
 
 // One work item: kv head g of group `it` = (sequence b, query tile qt, key tiles [tb, te),
 // partial group or -1).
-template <int G, bool PAGED, bool CAUSAL>
-__device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, const int g, lds_char* const (&KS)[2],
-                                             lds_char* const (&VS)[2], int wave, int lane) {
+template <int G, bool PAGED, bool CAUSAL, class LastStep, class AfterTiles, class AfterEpilogue>
+__device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, const int g, const int cuv,
+                                             const int bt_lane, lds_char* const (&KS)[2], lds_char* const (&VS)[2],
+                                             int wave, int lane,
+                                             LastStep&& last_step, AfterTiles&& after_tiles,
+                                             AfterEpilogue&& after_epilogue) {
   constexpr int D = kHeadDim;
   constexpr int TN = kTileKeys;
   constexpr int TM = kPrefillRows / G;
@@ -495,10 +502,19 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
   const int part = it.w < 0 ? -1 : it.w * a.num_kv_heads + g;
   // The work list is trusted only as far as the buffers reach: an entry naming a sequence or
   // key tiles outside this call (a workspace overwritten by an overlapping call) is skipped.
-  if (b < 0 || b >= a.num_seqs) return;
-  const SeqDims sd = seq_dims<TM>(a, b);
-  const int q0 = sd.q0, Lq = sd.Lq, k0 = sd.k0, Lk = sd.Lk, P = sd.P;
-  if (tb > te || te > (Lk + TN - 1) / TN) return;
+  // The hooks run in every case, so the work-group's barriers and claims stay in step.
+  // cuv (lanes 0..3) holds the sequence's bounds, loaded by the caller.
+  const int q0 = __builtin_amdgcn_readlane(cuv, 0);
+  const int Lq = __builtin_amdgcn_readlane(cuv, 1) - q0;
+  const int k0 = __builtin_amdgcn_readlane(cuv, 2);
+  const int Lk = min(__builtin_amdgcn_readlane(cuv, 3) - k0, a.max_seqlen_k);
+  const int P = Lk - Lq;
+  if (b < 0 || b >= a.num_seqs || Lq <= 0 || tb > te || te > (Lk + TN - 1) / TN) {
+    lds_barrier();
+    after_tiles();
+    after_epilogue();
+    return;
+  }
   const int tok_begin = qt * TM;
 
   const int col = lane & 31;   // MFMA column = this lane's query row inside a block
@@ -526,14 +542,6 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
     for (int kb = 0; kb < D / 16; ++kb)
       qb[rb][kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + kb * 16));
   }
-  // The sequence's first 64 block-table entries sit one per lane in a register, so a tile's
-  // block id is a readlane instead of a dependent global load.
-  int bt_lane = 0;
-  if constexpr (PAGED) {
-    const int nblk = (Lk + a.block_size - 1) / a.block_size;
-    if (lane < nblk) bt_lane = a.block_table[(int64_t)b * a.bt_stride + lane];
-  }
-
   f32x16 o[kRowBlocks][4];
   float m_i[kRowBlocks], l_i[kRowBlocks];
 #pragma unroll
@@ -565,6 +573,7 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
     for (int s = 0; s < 2; ++s) {
       const int n = n0 + s;
       if (n >= ntiles) break;
+      if (n == ntiles - 1) last_step();
       const int t0 = tbase + n * TN;
       KvRegs Rn;
       if (n + 2 < ntiles) load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, t0 + 2 * TN, ll, Rn);
@@ -581,6 +590,7 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
     }
   }
 
+  after_tiles();
   // Epilogue: O^T element rr of d-block md is d = 32 md + 8 (rr >> 2) + 4 half + (rr & 3).
 #pragma unroll
   for (int rb = 0; rb < kRowBlocks; ++rb) {
@@ -619,6 +629,7 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
             make_float2(m_i[rb], l_tot);
     }
   }
+  after_epilogue();
 }
 
 template <int G, bool PAGED, bool CAUSAL>
@@ -626,7 +637,7 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel
   // two stages per operand (constant stage indices put the stage offset in immediates)
   __shared__ __attribute__((aligned(1024))) char sK[2][kTileBytes];
   __shared__ __attribute__((aligned(1024))) char sV[2][kTileBytes];
-  __shared__ int s_item[2];  // alternating claim slots: one barrier per claim
+  __shared__ int s_item;  // the claimed item index
   lds_char* KS[2];
   lds_char* VS[2];
 #pragma unroll
@@ -638,34 +649,113 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  // Work-groups are dealt to the 8 XCDs round-robin by linear id: this one serves sub-queue
-  // blockIdx mod 8 first (items i = 8 j + x), then the others in turn. Every claim moves a
-  // counter forward, and a work-group leaves once all eight sub-queues are exhausted.
+  // Work-groups are dealt to the 8 XCDs round-robin by linear id: this one claims items of
+  // sub-queue x = blockIdx mod 8 (items i = 8 j + x, counter x) while it has any, then steals
+  // from the others. Wavefront 0 claims; lane 0 owns the atomics.
   const int xcd = blockIdx.x & 7;
-  const int num_items = (int)min((int64_t)a.pf_queue[8], (int64_t)a.pf_item_cap * a.num_kv_heads);
-  int sq = 0;
-  for (int it = 0;; it ^= 1) {
-    if (tid == 0) {
-      int idx = -1;
-      while (sq < 8) {
-        const int q = (xcd + sq) & 7;
-        const int64_t cand = (int64_t)atomicAdd(&a.pf_queue[q], 1) * 8 + q;
-        if (cand < num_items) {
-          idx = (int)cand;
-          break;
-        }
-        ++sq;
-      }
-      s_item[it] = idx;
+  const int num_items = (int)min((int64_t)a.pf_queue[kPrefillQueueMeta], (int64_t)a.pf_item_cap * a.num_kv_heads);
+  // The claim on the own sub-queue goes out when the current item starts its last key tile,
+  // so the atomic overlaps that tile and the work-group holds no item it cannot start yet
+  // (items are long: a claim made earlier would hold one back from idle work-groups at the
+  // end). `pend` is that atomic's result (lane 0).
+  bool own = true;
+  int pend = 0;
+  const auto claim_issue = [&]() {
+    if (wave == 0 && own && lane == 0) pend = atomicAdd(&a.pf_queue[xcd * kPrefillQueueStride], 1);
+  };
+  // Wavefront 0: the claimed index, or -1 once every sub-queue is exhausted. Stealing reads
+  // the other seven counters at once (lanes 0..6) and takes from the first sub-queue after
+  // this one that has items left; a claim that lost the race reads again. Counters only
+  // grow, so a stale read never shows a sub-queue exhausted too early.
+  const auto claim_finish = [&]() {
+    if (own) {
+      const int64_t cand = (int64_t)__builtin_amdgcn_readfirstlane(pend) * 8 + xcd;
+      if (cand < num_items) return (int)cand;
+      own = false;
     }
-    // Slot `it` is rewritten two claims later, after the next claim's barrier, which every
-    // wavefront passes only once it has read this one. Pending stores of the previous item
-    // need not drain here.
-    lds_barrier();
-    const int idx = __builtin_amdgcn_readfirstlane(s_item[it]);
-    if (idx < 0) break;
+    for (;;) {
+      const int q = (xcd + 1 + lane) & 7;
+      const int c = lane < 7 ? __hip_atomic_load(&a.pf_queue[q * kPrefillQueueStride], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)
+                             : 0;
+      const uint64_t left = __builtin_amdgcn_ballot_w64(lane < 7 && (int64_t)c * 8 + q < num_items);
+      if (left == 0) return -1;
+      const int qs = (xcd + 1 + __builtin_ctzll(left)) & 7;
+      int r = 0;
+      if (lane == 0) r = atomicAdd(&a.pf_queue[qs * kPrefillQueueStride], 1);
+      const int64_t cand = (int64_t)__builtin_amdgcn_readfirstlane(r) * 8 + qs;
+      if (cand < num_items) return (int)cand;
+    }
+  };
+  if (wave == 0) {
+    claim_issue();
+    const int c = claim_finish();
+    if (lane == 0) s_item = c;
+  }
+  lds_barrier();
+  // The next item's inputs load in two dependent steps around the current item's epilogue:
+  // its work-list group (lanes 0..3) before the epilogue's stores, then the sequence's
+  // bounds (lanes 0..3: cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]) and first 64
+  // block-table entries (one per lane: a tile's block id is a readlane, not a dependent
+  // global load) after them.
+  const auto load_group = [&](int i) {
+    return lane < 4 ? reinterpret_cast<const int*>(a.pf_items)[(int64_t)(i / a.num_kv_heads) * 4 + lane] : 0;
+  };
+  // The work list is trusted only as far as the buffers reach: a group naming a sequence
+  // outside this call (a workspace overwritten by an overlapping call) reads sequence 0's
+  // bounds and is skipped by prefill_item.
+  const auto seq_of = [&](int grpv) {
+    const int b = __builtin_amdgcn_readlane(grpv, 0);
+    return b >= 0 && b < a.num_seqs ? b : 0;
+  };
+  const auto load_bounds = [&](int b) {
+    const int32_t* p = lane < 2 ? a.cu_q + b + lane : a.cu_k + b + (lane - 2);
+    return lane < 4 ? *p : 0;
+  };
+  const auto load_bt = [&](int b) {
+    if constexpr (!PAGED) return 0;
+    return lane < min(a.bt_stride, kWave) ? a.block_table[(int64_t)b * a.bt_stride + lane] : 0;
+  };
+  int idx = __builtin_amdgcn_readfirstlane(s_item);
+  int grpv = 0, cuv = 0, btv = 0;
+  if (idx >= 0) {
+    grpv = load_group(idx);
+    cuv = load_bounds(seq_of(grpv));
+    btv = load_bt(seq_of(grpv));
+  }
+  while (idx >= 0) {
+    int next = -1, next_grpv = 0, next_cuv = 0, next_btv = 0;
+    bool claimed = false;
     const int grp = idx / a.num_kv_heads;
-    prefill_item<G, PAGED, CAUSAL>(a, a.pf_items[grp], idx - grp * a.num_kv_heads, KS, VS, wave, lane);
+    const int4 it = make_int4(__builtin_amdgcn_readlane(grpv, 0), __builtin_amdgcn_readlane(grpv, 1),
+                              __builtin_amdgcn_readlane(grpv, 2), __builtin_amdgcn_readlane(grpv, 3));
+    prefill_item<G, PAGED, CAUSAL>(
+        a, it, idx - grp * a.num_kv_heads, cuv, btv, KS, VS, wave, lane,
+        [&]() {
+          claim_issue();
+          claimed = true;
+        },
+        [&]() {
+          // s_item was last read before this item's first barrier
+          if (wave == 0) {
+            if (!claimed) claim_issue();
+            const int c = claim_finish();
+            if (lane == 0) s_item = c;
+          }
+          lds_barrier();
+          next = __builtin_amdgcn_readfirstlane(s_item);
+          if (next >= 0) next_grpv = load_group(next);
+        },
+        [&]() {
+          if (next >= 0) {
+            next_cuv = load_bounds(seq_of(next_grpv));
+            next_btv = load_bt(seq_of(next_grpv));
+          }
+        });
+    idx = next;
+    grpv = next_grpv;
+    cuv = next_cuv;
+    btv = next_btv;
   }
 }
 
@@ -680,7 +770,7 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
   constexpr int D = kHeadDim;
   constexpr int TM = kPrefillRows / G;
   constexpr int CQ = 8;  // chunks per quarter
-  const int nw = (int)min((int64_t)a.pf_queue[9], (int64_t)a.pf_merge_cap * a.num_kv_heads) * 4;
+  const int nw = (int)min((int64_t)a.pf_queue[kPrefillQueueMeta + 1], (int64_t)a.pf_merge_cap * a.num_kv_heads) * 4;
   const int r = threadIdx.x;
   const int hkv = a.num_kv_heads;
   // w = (unit, quarter) * hkv + g: with 8 kv heads, head g's merges run on XCD g (work-groups
