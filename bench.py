@@ -225,6 +225,23 @@ def cpu_baselines(dev, gpu_kernels: dict | None, reps: int = 3) -> dict:
     return res
 
 
+def prefill_probe(dev) -> int:
+    """5 calls each of cfg3's prefill part and the prefill_steady batch (counter passes)."""
+    import torch
+
+    from pagedkv.workloads import make_workload
+
+    for name in ("cfg3", "prefill_steady"):
+        w = make_workload(name, dev)
+        call = attention_call(w, sub_batch(w, lambda i: w.q_lens[i] > 1)) if name == "cfg3" else attention_call(w)
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+        log(f"[bench] prefill probe: {name} done")
+        del w
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -236,6 +253,8 @@ def main() -> int:
     ap.add_argument("--e2e-only", action="store_true",
                     help="only the end-to-end serving run (prints its JSON object), for profiling")
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only run 5 cfg3 prefill calls and 5 prefill_steady calls, for rocprofv3 --pmc passes")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 cfg2 decode calls and 5 copies of 1 GiB (the counter calibration), "
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
@@ -255,6 +274,8 @@ def main() -> int:
     if args.e2e_only:
         print(json.dumps(run_e2e(dev)), flush=True)
         return 0
+    if args.prefill_probe:
+        return prefill_probe(dev)
     log("[bench] building cfg2 (256 seqs, Lk ~ U[1024, 8192]) on the GPU")
     w = make_workload("cfg2", dev)
     if args.pmc_probe:
@@ -510,6 +531,13 @@ def extra_configs(dev, w2):
     fl = w3.prefill_flops()
     res["cfg3_prefill"] = {"ms": round(ms_p, 5), "TFLOP/s": round(fl / ms_p / 1e9, 2),
                            "mfma_frac": round(fl / ms_p / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4), "flops": fl}
+    ws_ = make_workload("prefill_steady", dev)
+    ms_s, _ = timed_launches(attention_call(ws_), 10)
+    fl_s = ws_.prefill_flops()
+    res["prefill_steady"] = {"ms": round(ms_s, 5), "TFLOP/s": round(fl_s / ms_s / 1e9, 2),
+                             "mfma_frac": round(fl_s / ms_s / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4), "flops": fl_s,
+                             "batch": "16 chunks of 1024 tokens over 4096-token cached prefixes"}
+    del ws_
     ms_d, _ = timed_launches(attention_call(w3, sub_batch(w3, lambda i: w3.q_lens[i] == 1)), 20)
     kvb = w3.decode_kv_bytes()
     res["cfg3_decode"] = {"ms": round(ms_d, 5), "GB/s": round(kvb / ms_d / 1e6, 1), "seqs": n_dec}

@@ -31,7 +31,7 @@ from .context import Context
 HQ, HKV, HEAD_DIM, BLOCK_SIZE = 16, 8, 128, 256   # Qwen3-0.6B attention geometry
 ROW_BYTES = HKV * HEAD_DIM * 2                     # one token row of K (or V), bytes
 
-WORKLOADS = ("cfg1_store", "cfg1_decode", "cfg2", "cfg3", "cfg4")
+WORKLOADS = ("cfg1_store", "cfg1_decode", "cfg2", "cfg3", "cfg4", "prefill_steady")
 
 
 @dataclass
@@ -196,7 +196,7 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
     """Build one of WORKLOADS. num_seqs shrinks the batch (tests); None = full size."""
     if name not in WORKLOADS:
         raise ValueError(f"unknown workload {name!r}; choose from {WORKLOADS}")
-    cfg_seed = {"cfg1_store": 1, "cfg1_decode": 1, "cfg2": 2, "cfg3": 3, "cfg4": 4}[name]
+    cfg_seed = {"cfg1_store": 1, "cfg1_decode": 1, "cfg2": 2, "cfg3": 3, "cfg4": 4, "prefill_steady": 5}[name]
     seed = cfg_seed if seed is None else seed
     host = torch.Generator()
     host.manual_seed(seed)
@@ -242,6 +242,17 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
         seqs += [(chunk, lk, bt) for lk, bt in zip(lks[n_dec:], tables[n_dec:])]
         return _assemble(name, seqs, nb, seed * 1000 + 3, device, unique_blocks=0,
                          meta={"prefixes": prefixes})
+
+    if name == "prefill_steady":
+        # chunked prefill large enough to keep every CU busy: 16 chunks of 1024 tokens, each
+        # over a 4096-token cached prefix (618 GFLOP of causal attention)
+        s = 16 if num_seqs is None else num_seqs
+        chunk, prefix = 1024, 4096
+        lks = [prefix + chunk] * s
+        nb = sum(math.ceil(lk / BLOCK_SIZE) for lk in lks)
+        pool = torch.randperm(nb, generator=host).tolist()
+        tables = _pop_tables(lks, pool)
+        return _assemble(name, [(chunk, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 5, device)
 
     # cfg4: 64 sequences share one 2048-token prefix (8 physical blocks, refcount 64);
     # private suffixes of U[256, 1024] tokens.
