@@ -154,6 +154,20 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// Maximum over the 16 lanes of a DPP row; every lane of the row receives it.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return v;
+}
+
+// Lane `l`'s value (l a compile-time constant), in a scalar register for the wavefront.
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 __device__ __forceinline__ float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
 }  // namespace pk

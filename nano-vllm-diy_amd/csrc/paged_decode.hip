@@ -493,23 +493,22 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
     // Every load of the merge is issued at once: lane j < nsplit of each wavefront reads
     // split j's (max, sum), thread d element d of every split. The weights are formed in
     // lanes 0 .. kCombineFast - 1 and broadcast by shuffles: no LDS, no barrier.
+    // Reductions are DPP row steps plus reads of the four rows' lanes, and weight j reaches
+    // every lane by a readlane: no LDS permutes on the dependency chain.
     const int lane = threadIdx.x & (kWave - 1);
     float2 ml = make_float2(-INFINITY, 0.f);
     if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)slot_of(lane) * H) * 2);
     float v[kCombineFast];
 #pragma unroll
     for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[(int64_t)slot_of(j) * stride] : 0.f;
-    float mx = ml.x;
-#pragma unroll
-    for (int m = kCombineFast / 2; m >= 1; m >>= 1) mx = fmaxf(mx, xor_shfl(mx, m));
+    const float rm = row16_max(ml.x);
+    const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
     const float w = lane < nsplit ? exp2_fast(ml.x - mx) : 0.f;
-    float ls = w * ml.y;
-#pragma unroll
-    for (int m = kCombineFast / 2; m >= 1; m >>= 1) ls += xor_shfl(ls, m);
-    const float lsum = __shfl(ls, 0, kWave);
+    const float rs = row16_sum(w * ml.y);
+    const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
     float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < kCombineFast; ++j) acc = fmaf(__shfl(w, j, kWave), v[j], acc);
+    for (int j = 0; j < kCombineFast; ++j) acc = fmaf(lane_value(w, j), v[j], acc);
     a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(acc / lsum);
     return;
   }
