@@ -372,8 +372,10 @@ __device__ __forceinline__ int split_begin(int t, int n, int s) { return (int)((
 
 // Length bucket of a group of t tiles (0 = longest) for split size T.
 __device__ __forceinline__ int length_bucket(int t, int T) {
-  const int j = (int)min((int64_t)kBuckets - 1, ((int64_t)t * kBuckets + T - 1) / T - 1);  // ceil(t K / T) - 1
-  return kBuckets - 1 - max(0, j);
+  int j = 0;  // the largest j < kBuckets with t kBuckets > j T (compares, no division)
+#pragma unroll
+  for (int i = 1; i < kBuckets; ++i) j = t * kBuckets > i * T ? i : j;
+  return kBuckets - 1 - j;
 }
 
 // Work list. Waves take sequences in turn and lanes take a sequence's query tiles, so a
