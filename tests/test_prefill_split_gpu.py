@@ -126,3 +126,23 @@ def test_workspace_reuse_after_split_call(gpu):
             got = _run(gpu, *a, s, workspace=shared)
             torch.cuda.synchronize()
             assert bits_equal(got, want), f"rep {rep} seqs {s}"
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 2), (8, 1)])
+def test_many_small_items_exhaust_and_steal(gpu, hq, hkv):
+    """Hundreds of short prompts over short cached prefixes: several items per work-group,
+    so every work-group claims past its own sub-queue's end and steals from the others."""
+    rng = np.random.default_rng(hq * 10 + hkv)
+    seqs = []
+    for i in range(300):
+        lq = int(rng.integers(2, 41))
+        seqs.append((lq, lq + int(rng.integers(0, 300))))
+    _check(gpu, seqs, hq, hkv, seed=hkv, what=f"300 small prompts hkv={hkv}")
+
+
+@pytest.mark.parametrize("hkv", [1, 8])
+def test_fewer_items_than_work_groups(gpu, hkv):
+    """One 2-token prompt (a single work item for hkv = 1): every other work-group finds all
+    sub-queues empty on its first claim and leaves."""
+    _check(gpu, [(2, 3)], 8 if hkv == 1 else 16, hkv, seed=3, what=f"one item hkv={hkv}")
+    _check(gpu, [(2, 2), (1, 7), (3, 300)], 8 if hkv == 1 else 16, hkv, seed=4, what=f"three seqs hkv={hkv}")
