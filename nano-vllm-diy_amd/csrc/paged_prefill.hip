@@ -486,7 +486,9 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const AttnAr
 }
 
 // One work item: kv head g of group `it` = (sequence b, query tile qt, key tiles [tb, te),
-// partial group or -1).
+// partial group or -1). The caller's hooks run at three points, which the kernel uses to
+// claim and prefetch the next item: last_step when the last key tile starts, after_tiles
+// after the last tile's barrier (before the epilogue), after_epilogue after its stores.
 template <int G, bool PAGED, bool CAUSAL, class LastStep, class AfterTiles, class AfterEpilogue>
 __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, const int g, const int cuv,
                                              const int bt_lane, lds_char* const (&KS)[2], lds_char* const (&VS)[2],
