@@ -37,13 +37,18 @@ class LLMEngine:
                  num_blocks: int | None = None, block_size: int = 256, max_num_seqs: int = 512,
                  max_num_batched_tokens: int = 16384, chunked_prefill_size: int = 512,
                  max_live_seqs: int = 128, max_seq_len: int = 8192, enforce_eager: bool = False,
-                 eos: int = 151645, seed: int = 5):
+                 eos: int = 151645, seed: int = 5, gpu_memory_utilization: float | None = None):
+        """num_blocks None: with gpu_memory_utilization, as many blocks as fit in that share of
+        the device (the reference's sizing, model_runner.py:149-157); without it, enough for
+        max_live_seqs sequences of max_seq_len tokens."""
         # RunnerConfig caps the model's context at 8192 (runner_config.py:13,41)
         self.max_seq_len = min(max_seq_len, cfg.max_position_embeddings)
-        if num_blocks is None:
+        if num_blocks is None and gpu_memory_utilization is None:
             num_blocks = max_live_seqs * ((self.max_seq_len + block_size - 1) // block_size)
         self.runner = ModelRunner(cfg, device, num_blocks, block_size, self.max_seq_len,
-                                  min(max_num_seqs, max_live_seqs, 512), enforce_eager, seed)
+                                  min(max_num_seqs, max_live_seqs, 512), enforce_eager, seed,
+                                  gpu_memory_utilization or 0.9)
+        num_blocks = self.runner.num_blocks
         self.scheduler = HostScheduler(num_blocks, block_size, max_num_seqs, max_num_batched_tokens,
                                        chunked_prefill_size, max_live_seqs, eos, self.max_seq_len)
 

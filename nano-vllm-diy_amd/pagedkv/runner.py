@@ -41,18 +41,48 @@ def context_buckets(max_seq_len: int, smallest: int = 512) -> list[int]:
     return out + [max_seq_len]
 
 
+def kv_cache_num_blocks(num_layers: int, block_size: int, num_kv_heads: int, head_dim: int,
+                        gpu_memory_utilization: float = 0.9, requested: int | None = None,
+                        itemsize: int = 2, device: torch.device | str | None = None) -> int:
+    """KV-cache blocks that fit in gpu_memory_utilization of the device, as the reference
+    sizes its cache (model_runner.py:149-157): total x utilization, minus what is in use,
+    minus the allocator's peak beyond its current allocation (the activations a forward pass
+    needs on top of the weights), divided by one block's K and V over all layers. A request
+    above that raises, as the reference's assert does; requested None or <= 0 takes them all.
+    """
+    free, total = torch.cuda.mem_get_info(device)
+    used = total - free
+    stats = torch.cuda.memory_stats(device)
+    peak = stats["allocated_bytes.all.peak"]
+    current = stats["allocated_bytes.all.current"]
+    block_bytes = 2 * num_layers * block_size * num_kv_heads * head_dim * itemsize
+    max_blocks = int(total * gpu_memory_utilization - used - peak + current) // block_bytes
+    if requested is None or requested <= 0:
+        requested = max_blocks
+    if requested > max_blocks:
+        raise RuntimeError(f"Not enough GPU memory to allocate kv cache, required "
+                           f"{requested * block_bytes / 2**30:.2f} GB but only "
+                           f"{max_blocks * block_bytes / 2**30:.2f} GB is available")
+    return requested
+
+
 class ModelRunner:
-    def __init__(self, cfg: Qwen3Config, device: torch.device | str, num_blocks: int,
+    def __init__(self, cfg: Qwen3Config, device: torch.device | str, num_blocks: int | None,
                  block_size: int = 256, max_seq_len: int = 8192, max_graph_bs: int = 128,
-                 enforce_eager: bool = False, seed: int = 5):
+                 enforce_eager: bool = False, seed: int = 5, gpu_memory_utilization: float = 0.9):
+        """num_blocks None: as many cache blocks as fit in gpu_memory_utilization of the
+        device once the weights are in place (kv_cache_num_blocks)."""
         self.cfg = cfg
         self.dev = torch.device(device)
         self.block_size = block_size
         self.max_seq_len = max_seq_len
         L, Hkv, D = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+        self.weights = Qwen3Weights(cfg, self.dev, seed)
+        if num_blocks is None:
+            num_blocks = kv_cache_num_blocks(L, block_size, Hkv, D, gpu_memory_utilization, device=self.dev)
+        self.num_blocks = num_blocks
         self.kv_cache = torch.empty(2, L, num_blocks, block_size, Hkv, D, dtype=torch.bfloat16,
                                     device=self.dev)
-        self.weights = Qwen3Weights(cfg, self.dev, seed)
         self.model = Qwen3Model(cfg, self.weights, self.kv_cache[0], self.kv_cache[1],
                                 cfg.max_position_embeddings)
         self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}

@@ -70,3 +70,27 @@ def test_engine_graph_padding_and_block_crossing(gpu):
     assert [len(o) for o in outs] == [10, 8, 4]
     assert eng.scheduler.num_free_blocks() == 32
     _check(eng, cfg, prompts, outs)
+
+
+def test_engine_sizes_kv_cache_from_free_memory(gpu):
+    """num_blocks None with gpu_memory_utilization: the cache takes what fits in that share
+    of the device after the weights (model_runner.py:149-157), and the engine serves from it."""
+    from pagedkv.runner import kv_cache_num_blocks
+
+    cfg = Qwen3Config(num_hidden_layers=2)
+    free, total = torch.cuda.mem_get_info(gpu)
+    util = (total - free) / total + 0.02                  # about 2% of the device for the cache
+    eng = E.LLMEngine(cfg, device=gpu, max_live_seqs=8, max_seq_len=1024, enforce_eager=True,
+                      gpu_memory_utilization=util)
+    nb = eng.runner.num_blocks
+    block_bytes = 2 * cfg.num_hidden_layers * 256 * cfg.num_key_value_heads * cfg.head_dim * 2
+    assert nb > 0 and nb * block_bytes <= total * util
+    assert eng.runner.kv_cache.shape[2] == nb
+    # nothing is left for a second cache of the same size at the same utilisation
+    with pytest.raises(RuntimeError, match="Not enough GPU memory"):
+        kv_cache_num_blocks(cfg.num_hidden_layers, 256, cfg.num_key_value_heads, cfg.head_dim, util,
+                            requested=nb, device=gpu)
+    rng = random.Random(4)
+    prompts = [[rng.randrange(cfg.vocab_size) for _ in range(n)] for n in (40, 200)]
+    outs, _ = eng.generate(prompts, [4, 6], ignore_eos=True)
+    assert [len(o) for o in outs] == [4, 6]

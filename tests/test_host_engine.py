@@ -249,3 +249,28 @@ def test_host_core_rejects_bad_calls():
     core.postprocess([4])
     assert core.generated(sid) == [4]
     assert torch.is_tensor(st.input_ids)
+
+
+def test_kv_cache_sizing_follows_reference_formula(monkeypatch):
+    """model_runner.py:149-157: blocks = (total x util - used - peak + current) // block_bytes,
+    block_bytes = 2 x layers x block_size x kv_heads x head_dim x itemsize; a request above
+    that raises; None or <= 0 takes the maximum."""
+    import torch
+    from pagedkv.runner import kv_cache_num_blocks
+
+    gib = 1 << 30
+    total, free = 288 * gib, 280 * gib
+    stats = {"allocated_bytes.all.peak": 3 * gib, "allocated_bytes.all.current": 2 * gib}
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (free, total))
+    monkeypatch.setattr(torch.cuda, "memory_stats", lambda device=None: stats)
+    block_bytes = 2 * 28 * 256 * 8 * 128 * 2                      # Qwen3-0.6B, block 256, bf16
+    budget = int(total * 0.9 - (total - free) - 3 * gib + 2 * gib)
+    want = budget // block_bytes
+    assert kv_cache_num_blocks(28, 256, 8, 128, 0.9) == want
+    assert kv_cache_num_blocks(28, 256, 8, 128, 0.9, requested=0) == want
+    assert kv_cache_num_blocks(28, 256, 8, 128, 0.9, requested=100) == 100
+    with pytest.raises(RuntimeError, match="Not enough GPU memory"):
+        kv_cache_num_blocks(28, 256, 8, 128, 0.9, requested=want + 1)
+    # the activation headroom counts: a higher peak leaves fewer blocks
+    stats["allocated_bytes.all.peak"] = 10 * gib
+    assert kv_cache_num_blocks(28, 256, 8, 128, 0.9) == (budget - 7 * gib) // block_bytes
