@@ -52,22 +52,33 @@ struct WorkspaceLayout {
   int64_t pf_item_cap;
   size_t pf_queue_off, pf_items_off, pf_merges_off, pf_part_o_off, pf_part_ml_off;
   size_t sp_plan_off;
+  pk::FlatDecodePlan flat;  // flat decode grid (flat.groups == 0: split grid only)
+  size_t flat_meta_off;
   size_t total;
 };
 
-// [decode: per-split partial numerators | per-split (max, sum) | shared-prefix plan]  (empty
-// when no sequence can have more than one split: those write their output directly)
+// [decode: partial numerators | partial (max, sum) | flat-grid record | shared-prefix plan]
+// (empty when no sequence can have more than one split: those write their output directly;
+// the partial regions hold the split grid's num_seqs x max_splits units or the flat grid's
+// num_seqs + groups, whichever is larger)
 // [prefill: queue header | work items | merge list | partial numerators | (max, sum)]
 WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_q, int max_seqlen_k) {
   WorkspaceLayout w{};
   w.split_tokens = pk::decode_split_tokens(num_seqs, max_seqlen_k);
   w.max_splits = max_seqlen_k > 0 ? (max_seqlen_k + w.split_tokens - 1) / w.split_tokens : 0;
+  w.flat = pk::decode_flat_plan(num_seqs, max_seqlen_k);  // groups > 0 only when max_splits > 1
   if (w.max_splits > 1) {  // single-split sequences write their output directly
-    const size_t units = (size_t)num_seqs * (size_t)w.max_splits * (size_t)num_heads;
+    size_t seq_units = (size_t)num_seqs * (size_t)w.max_splits;
+    if (w.flat.groups > 0) seq_units = std::max(seq_units, (size_t)num_seqs + (size_t)w.flat.groups);
+    const size_t units = seq_units * (size_t)num_heads;
     w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
     w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
   }
   size_t off = w.part_o_bytes + w.part_ml_bytes;
+  if (w.flat.groups > 0) {  // the run length the flat grid used, for the combine
+    w.flat_meta_off = off;
+    off += kWorkspaceAlign;
+  }
   if (w.max_splits > 1) {  // the shared-prefix plan: at most one item per (sequence, slot)
     w.sp_plan_off = off;
     off += round_up(pk::shared_prefix_plan_bytes(num_seqs, w.max_splits), kWorkspaceAlign);
@@ -376,6 +387,11 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   if (ws.part_o_bytes > 0) {
     a.part_o = reinterpret_cast<float*>(wsb);
     a.part_ml = reinterpret_cast<float*>(wsb + ws.part_o_bytes);
+  }
+  if (a.prefix_keys == 0 && ws.flat.groups > 0) {  // the flat decode grid (the shared-prefix path splits)
+    a.flat_groups = ws.flat.groups;
+    a.flat_min_chunk = ws.flat.min_chunk;
+    a.flat_meta = reinterpret_cast<int32_t*>(wsb + ws.flat_meta_off);
   }
   if (max_seqlen_q > 1) {
     a.pf_queue = reinterpret_cast<int32_t*>(wsb + ws.pf_queue_off);

@@ -47,6 +47,16 @@ struct AttnArgs {
   int32_t split_tokens;
   int32_t max_splits;           // partial slots per sequence (stride of part_o / part_ml)
   int32_t grid_splits;          // splits the decode grid covers per sequence
+  // Flat decode grid (flat_groups > 0, no shared prefix): work-group w takes the keys at
+  // positions [w * chunk, (w + 1) * chunk) of the batch's key line (key t of sequence b at
+  // cu_k[b] + t); a sequence's piece in work-group w is partial unit b + w
+  // (part_o: [num_seqs + flat_groups][num_heads][head_dim]). chunk >= flat_min_chunk is set
+  // on the device from the largest cu_k entry and kept in flat_meta[0] for the combine;
+  // flat_step = keys per pipeline step (set by the decode launch).
+  int32_t flat_groups;
+  int32_t flat_min_chunk;
+  int32_t flat_step;
+  int32_t* flat_meta;
   // Shared-prefix decode: keys [0, min(prefix_keys, Lk)) of a decode sequence are computed by
   // the shared-prefix kernel, one partial per chunk of prefix_chunk keys in slots
   // [0, prefix_slots); the split kernel covers the keys after them, its split s in slot
@@ -193,6 +203,12 @@ hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal,
                           int max_seqlen_q, hipStream_t stream);
 // Split size (keys per work-group) the decode kernel uses for these launch bounds.
 int decode_split_tokens(int num_seqs, int max_seqlen_k);
+// Flat decode grid for these launch bounds: groups == 0 when the split grid is used.
+struct FlatDecodePlan {
+  int groups;
+  int min_chunk;
+};
+FlatDecodePlan decode_flat_plan(int num_seqs, int max_seqlen_k);
 // Per-head RMSNorm + RoPE of q and k from the fused qkv row, K/V rows into their slots.
 hipError_t launch_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride,
                                      const int64_t* positions, const float* cos_sin,

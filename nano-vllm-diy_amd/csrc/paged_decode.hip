@@ -22,6 +22,8 @@
 //   * softmax: keys of a step are lane-local, so the running max needs no shuffles.
 //   * P.V: p rounded to bf16 and paired across two keys, one dot2 per (head, element).
 // Loads are software-pipelined two steps deep and all issued before the step's math.
+#include <algorithm>
+
 #include "norm_rope.h"
 
 namespace pk {
@@ -42,6 +44,27 @@ namespace {
 #endif
 #ifndef PK_DECODE_MIN_SPLIT
 #define PK_DECODE_MIN_SPLIT 64     // shortest split (keys) the sizing goes down to
+#endif
+// Flat decode grid (below): used for batches of at most PK_DECODE_FLAT_MAX_SEQS sequences
+// whose launch bound (num_seqs x max_seqlen_k) holds at least PK_DECODE_FLAT_MIN_KEYS keys.
+// Measured (us, split grid vs flat grid of 1024 work-groups, cold caches): 128 sequences of
+// 100-1024 keys 69.5 vs 64.7, of 100-2048 108.7 vs 98.2; 64 of 100-2048 68.0 vs 60.2; 32 of
+// 100-4096 66.8 vs 59.0; 16 of 1024-8192 80.5 vs 73.3; the 128 decodes of the mixed
+// chunked-prefill batch 222 vs 209. The split grid stays ahead for 256 sequences (100-2048
+// keys 213 vs 218; 1024-8192 keys 781 vs 789 with 1536 work-groups) and for 8 sequences of
+// 256-2048 keys (18.8 vs 21.8: too few keys to pay for the flat prologue's extra round trip).
+// Flat grids of 512, 768 and 1280 work-groups were each slower on most of these batches.
+#ifndef PK_DECODE_FLAT_MAX_SEQS
+#define PK_DECODE_FLAT_MAX_SEQS 192
+#endif
+#ifndef PK_DECODE_FLAT_MIN_KEYS
+#define PK_DECODE_FLAT_MIN_KEYS 32768
+#endif
+#ifndef PK_DECODE_FLAT_GROUPS
+#define PK_DECODE_FLAT_GROUPS 1024   // work-groups (runs + sequences) a flat decode launch aims for
+#endif
+#ifndef PK_DECODE_FLAT_MIN_CHUNK
+#define PK_DECODE_FLAT_MIN_CHUNK 32  // shortest run of keys per flat work-group
 #endif
 
 constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
@@ -318,36 +341,15 @@ __device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>
   }
 }
 
+// One work unit: keys [t_begin, t_end) of decode sequence b (query row q0, keys from k0 in
+// flat mode, Lk keys in all) for the kv heads of this wavefront. direct: the unit holds every
+// key of the sequence, so it normalises and writes the output row itself; otherwise it
+// leaves its (max, sum, numerator) partial at partial unit unit0 (x num_heads) for the combine.
 template <int G, int U, bool PAGED, bool FUSED>
-__global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
+__device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_first, int b, int q0, int k0, int Lk,
+                                            int t_begin, int t_end, bool direct, int64_t unit0) {
   static_assert(U % 2 == 0, "P.V pairs keys");
   constexpr int D = kHeadDim;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
-  // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
-  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
-  // Work-groups are dispatched round-robin over the 8 XCDs in linear id order. Split-major
-  // order with the sequence rotated by the split index sends consecutive splits of one
-  // sequence to consecutive XCDs, so every XCD gets about 1/8 of each sequence whatever the
-  // lengths (a (split, sequence) grid with 16 splits would give XCD k splits k and k+8 of
-  // every sequence: split 0 always exists, split 15 only for the longest contexts).
-  const int split = blockIdx.x / a.num_seqs;
-  const int b = (blockIdx.x - split * a.num_seqs + split) % a.num_seqs;
-  // Both length pairs are read before the first branch, in one round of scalar loads: the
-  // two early exits are one test, so neither pair waits behind the other's branch.
-  const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
-  const int k0 = a.cu_k[b], k1 = a.cu_k[b + 1];
-  const int Lk = min(k1 - k0, a.max_seqlen_k);
-  // keys below Pb belong to the shared-prefix kernel (Pb = 0 when it is off)
-  const int Pb = max(0, min(a.prefix_keys, Lk));
-  const int t_begin = Pb + split * a.split_tokens;
-  // rows with Lq != 1 belong to the prefill kernel; t_begin >= Lk also skips Lk <= 0 (graph padding)
-  if ((q1 - q0 != 1) | (t_begin >= Lk)) return;
-  const int t_end = min(Lk, t_begin + a.split_tokens);
-  // partials of the sequence: its prefix chunks, then its splits
-  const int nsplit = (Pb + a.prefix_chunk - 1) / a.prefix_chunk + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
-  const int slot = a.prefix_slots + split;
-
   const int c = lane & 15;
   const int g_lane = g_first + (lane >> 4);               // this DPP row's kv head
   const bool row_live = g_lane < a.num_kv_heads;
@@ -403,15 +405,14 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   }
 
   if (!row_live) return;
-  // Partials of this (sequence, split): H heads x (D numerators, (max, sum)), contiguous,
-  // written through L2 or left in it by the launch's choice (kStoreThroughBytes).
-  const int64_t unit0 = ((int64_t)b * a.max_splits + slot) * H;
+  // Partials of this unit: H heads x (D numerators, (max, sum)), contiguous, written
+  // through L2 or left in it by the launch's choice (kStoreThroughBytes).
   const __amdgpu_buffer_rsrc_t po_rs = row_rsrc(a.part_o + unit0 * D, (uint32_t)(H * D * 4));
   const __amdgpu_buffer_rsrc_t pml_rs = row_rsrc(a.part_ml + unit0 * 2, (uint32_t)(H * 8));
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int h = g * G + i;
-    if (nsplit == 1) {  // the only split of this sequence: normalise and store
+    if (direct) {  // the only unit of this sequence: normalise and store
       const float inv = 1.f / st.l[i];
       uint4 w;
       w.x = pack_bf16x2(st.acc[i][0] * inv, st.acc[i][1] * inv);
@@ -430,6 +431,129 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
         store_partial<0>(po_rs, pml_rs, o, h * 8, lo, hi, ml, c == 0);
     }
   }
+}
+
+// Split mode: grid (splits x sequences, kv-head groups); a work-group takes split `split` of
+// one sequence (split_tokens keys after the shared prefix, if any).
+template <int G, int U, bool PAGED, bool FUSED>
+__global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
+  // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
+  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
+  // Work-groups are dispatched round-robin over the 8 XCDs in linear id order. Split-major
+  // order with the sequence rotated by the split index sends consecutive splits of one
+  // sequence to consecutive XCDs, so every XCD gets about 1/8 of each sequence whatever the
+  // lengths (a (split, sequence) grid with 16 splits would give XCD k splits k and k+8 of
+  // every sequence: split 0 always exists, split 15 only for the longest contexts).
+  const int split = blockIdx.x / a.num_seqs;
+  const int b = (blockIdx.x - split * a.num_seqs + split) % a.num_seqs;
+  // Both length pairs are read before the first branch, in one round of scalar loads: the
+  // two early exits are one test, so neither pair waits behind the other's branch.
+  const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
+  const int k0 = a.cu_k[b], k1 = a.cu_k[b + 1];
+  const int Lk = min(k1 - k0, a.max_seqlen_k);
+  // keys below Pb belong to the shared-prefix kernel (Pb = 0 when it is off)
+  const int Pb = max(0, min(a.prefix_keys, Lk));
+  const int t_begin = Pb + split * a.split_tokens;
+  // rows with Lq != 1 belong to the prefill kernel; t_begin >= Lk also skips Lk <= 0 (graph padding)
+  if ((q1 - q0 != 1) | (t_begin >= Lk)) return;
+  const int t_end = min(Lk, t_begin + a.split_tokens);
+  // partials of the sequence: its prefix chunks, then its splits
+  const int nsplit = (Pb + a.prefix_chunk - 1) / a.prefix_chunk + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
+  const int slot = a.prefix_slots + split;
+  decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, nsplit == 1,
+                                  ((int64_t)b * a.max_splits + slot) * a.num_heads);
+}
+
+// Maximum of a non-negative int over the wavefront, in a scalar register.
+__device__ __forceinline__ int wave_max_nonneg(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppXor1, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppXor2, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppHalfMirror, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppMirror, 0xf, 0xf, false));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Flat mode: the batch's keys, at the positions cu_seqlens_k gives them (key t of sequence b
+// at cu_k[b] + t), are cut into W = flat_groups runs of `chunk` keys, so that the work is
+// spread evenly whatever the length mix (the split grid gives each sequence whole splits:
+// its last split is ragged, and short sequences leave many work-groups empty). A pipeline
+// step (U keys at a multiple of U inside its sequence) belongs to the run holding its first
+// key, so sequence b has a piece in runs w0(b) .. w1(b) (the runs of its first and last
+// steps). Piece (b, w) is work-group u = b + w and partial unit u: the index is unique
+// because both the runs and the sequences tile the key line in order, so
+// b + w1(b) < b' + w0(b') for b < b'. The grid has W + num_seqs work-groups; those whose
+// index falls between two sequences' ranges exit at once.
+// chunk = max(flat_min_chunk, ceil(T / W) rounded up to U), T = the largest cu_seqlens_k
+// entry (graph padding zeroes trailing entries, so the last one need not be the total);
+// work-group 0 records it for the combine. One wavefront holds every sequence's bounds
+// (num_seqs < 64 * kFlatSlots) and finds the work-group's sequence with one ballot per slot.
+constexpr int kFlatSlots = 8;
+
+template <int G, int U, bool PAGED, bool FUSED>
+__global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(const AttnArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;
+  const int n = a.num_seqs;
+  // lane l, slot s: sequence e = l + 64 s (bounds of both its key and query ranges)
+  int kb[kFlatSlots], ke[kFlatSlots], qb[kFlatSlots], qe[kFlatSlots];
+  int T = 0;
+#pragma unroll
+  for (int s = 0; s < kFlatSlots; ++s) {
+    kb[s] = ke[s] = qb[s] = qe[s] = 0;
+    if (64 * s <= n) {
+      const int e = lane + 64 * s;
+      if (e <= n) kb[s] = a.cu_k[e];
+      if (e < n) {
+        ke[s] = a.cu_k[e + 1];
+        qb[s] = a.cu_q[e];
+        qe[s] = a.cu_q[e + 1];
+      }
+      T = max(T, kb[s]);
+    }
+  }
+  T = wave_max_nonneg(T);
+  const int per = (int)(((int64_t)T + a.flat_groups - 1) / a.flat_groups);
+  const int chunk = max(a.flat_min_chunk, (per + U - 1) / U * U);
+  const int u = blockIdx.x;
+  // the decode sequence (Lq == 1, Lk > 0) with b + w0(b) <= u <= b + w1(b), if any
+  int b = -1, q0 = 0, k0 = 0, Lk = 0;
+#pragma unroll
+  for (int s = 0; s < kFlatSlots; ++s) {
+    if (64 * s < n) {
+      const int e = lane + 64 * s;
+      const int lk = min(ke[s] - kb[s], a.max_seqlen_k);
+      const bool dec = e < n && qe[s] - qb[s] == 1 && lk > 0 && kb[s] >= 0;
+      const int w0 = kb[s] / chunk;
+      const int w1 = (int)(((int64_t)kb[s] + (lk - 1) / U * U) / chunk);
+      const uint64_t m = __builtin_amdgcn_ballot_w64(dec && e + w0 <= u && u <= e + w1);
+      if (m) {
+        const int j = __builtin_ctzll(m);
+        b = 64 * s + j;
+        q0 = __builtin_amdgcn_readlane(qb[s], j);
+        k0 = __builtin_amdgcn_readlane(kb[s], j);
+        Lk = __builtin_amdgcn_readlane(lk, j);
+      }
+    }
+  }
+  // The record is written after the unit, so that no global store precedes its block-table
+  // reads: the compiler then knows the table unchanged and reads it with scalar loads.
+  const bool recorder = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0;
+  if (b < 0) {
+    if (recorder) a.flat_meta[0] = chunk;
+    return;
+  }
+  const int64_t F0 = (int64_t)(u - b) * chunk, F1 = F0 + chunk;  // this run's keys
+  const int64_t d = F0 - k0;
+  const int t_begin = d > 0 ? (int)((d + U - 1) / U * U) : 0;
+  const int t_end = (int)min<int64_t>(Lk, (F1 - k0 + U - 1) / U * U);
+  // the sequence's first and last steps in one run: this piece is all of it
+  const bool direct = k0 / chunk == ((int64_t)k0 + (Lk - 1) / U * U) / chunk;
+  decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct, (int64_t)u * a.num_heads);
+  if (recorder) a.flat_meta[0] = chunk;
 }
 
 // Merge the per-split partials of one (sequence, head). A separate launch (rather than a
@@ -477,15 +601,30 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   if (q1 - q0 != 1) return;
   const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
   if (Lk <= 0) return;
-  // partial j < npre: prefix chunk j (slot j); the others: split j - npre (slot prefix_slots + j - npre)
-  const int Pb = min(a.prefix_keys, Lk);
-  const int npre = (Pb + a.prefix_chunk - 1) / a.prefix_chunk;
-  const int nsplit = npre + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
-  if (nsplit <= 1 && npre == 0) return;  // written directly by the split kernel
-  const int gap = a.prefix_slots - npre;
-  const auto slot_of = [&](int j) { return j < npre ? j : j + gap; };
   const int H = a.num_heads;
-  const int64_t unit0 = (int64_t)b * a.max_splits * H + h;  // partial in slot j: unit0 + j H
+  int npre, nsplit, gap;
+  int64_t unit0;  // partial j of (sequence, head) at unit unit0 + slot_of(j) H
+  if (a.flat_groups > 0) {
+    // flat mode: the pieces of work-groups w0 .. w1 (those holding the first and the last
+    // step's first key), piece of work-group w at unit b + w
+    const int64_t chunk = a.flat_meta[0];
+    const int64_t w0 = max(0, k_lo) / chunk;
+    const int64_t w1 = ((int64_t)k_lo + (Lk - 1) / a.flat_step * a.flat_step) / chunk;
+    npre = 0;
+    gap = 0;
+    nsplit = (int)min<int64_t>(w1 - w0 + 1, kCombineMaxSplits);  // the plan keeps it <= kCombineMaxSplits
+    if (nsplit <= 1) return;  // written directly by the split kernel
+    unit0 = ((int64_t)b + w0) * H + h;
+  } else {
+    // partial j < npre: prefix chunk j (slot j); the others: split j - npre (slot prefix_slots + j - npre)
+    const int Pb = min(a.prefix_keys, Lk);
+    npre = (Pb + a.prefix_chunk - 1) / a.prefix_chunk;
+    nsplit = npre + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
+    if (nsplit <= 1 && npre == 0) return;  // written directly by the split kernel
+    gap = a.prefix_slots - npre;
+    unit0 = (int64_t)b * a.max_splits * H + h;
+  }
+  const auto slot_of = [&](int j) { return j < npre ? j : j + gap; };
   const int d = threadIdx.x;
   const float* po = a.part_o + unit0 * D + partial_slot(d);
   const int64_t stride = (int64_t)H * D;
@@ -540,15 +679,28 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
 
 template <int G, int U>
 hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
-  a.store_through = (int64_t)a.num_seqs * a.max_splits * a.num_heads * kHeadDim * 4 > kStoreThroughBytes;
+  const bool flat = a.flat_groups > 0;
+  const int64_t units = flat ? (int64_t)a.num_seqs + a.flat_groups : (int64_t)a.num_seqs * a.max_splits;
+  a.store_through = units * a.num_heads * kHeadDim * 4 > kStoreThroughBytes;
   const int quads = (a.num_kv_heads + 3) / 4;   // wavefronts needed for all kv heads
   int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
   while (quads % waves != 0) --waves;            // no idle wavefront in any work-group
   const int zgroups = quads / waves;
+  const dim3 block((unsigned)(waves * kWave));
+  const bool fused = a.qkv != nullptr || a.new_k != nullptr;  // paged only (checked by their entry points)
+  if (flat) {
+    const dim3 grid((unsigned)(a.flat_groups + a.num_seqs), (unsigned)zgroups);
+    if (fused)
+      hipLaunchKernelGGL((decode_flat_kernel<G, U, true, true>), grid, block, 0, stream, a);
+    else if (paged)
+      hipLaunchKernelGGL((decode_flat_kernel<G, U, true, false>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_flat_kernel<G, U, false, false>), grid, block, 0, stream, a);
+    return hipGetLastError();
+  }
   if (a.grid_splits <= 0) return hipSuccess;  // every decode key lies in the shared prefix
   const dim3 grid((unsigned)(a.grid_splits * a.num_seqs), (unsigned)zgroups);
-  const dim3 block((unsigned)(waves * kWave));
-  if (a.qkv != nullptr || a.new_k != nullptr)  // fused steps are paged only (checked by their entry points)
+  if (fused)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);
   else if (paged)
     hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, block, 0, stream, a);
@@ -556,6 +708,9 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
     hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
+
+// Keys per pipeline step of the decode kernels built for a GQA group.
+constexpr int decode_step_keys(int group) { return group <= 2 ? PK_DECODE_STEP_G2 : 4; }
 
 }  // namespace
 
@@ -572,19 +727,47 @@ int decode_split_tokens(int num_seqs, int max_seqlen_k) {
   return split;
 }
 
-hipError_t launch_decode(const AttnArgs& a, int group, bool paged, int max_seqlen_k,
+FlatDecodePlan decode_flat_plan(int num_seqs, int max_seqlen_k) {
+  // Flat mode needs every sequence bound in one wavefront (num_seqs < 64 * kFlatSlots), key
+  // positions that fit in 30 bits, and a batch the split grid would cut into several splits
+  // (a batch whose sequences each fit one split needs no partials at all); it is used in the
+  // measured range where it beats the split grid (PK_DECODE_FLAT_MAX_SEQS, _MIN_KEYS). Runs:
+  // enough that the grid (runs + sequences) is PK_DECODE_FLAT_GROUPS work-groups, or fewer
+  // when runs of PK_DECODE_FLAT_MIN_CHUNK keys cover the launch bound. The shortest run keeps
+  // a sequence within the combine's kCombineMaxSplits pieces: (Lk - 1) / chunk + 2 of them.
+  FlatDecodePlan p{0, 0};
+  if (num_seqs <= 0 || num_seqs > PK_DECODE_FLAT_MAX_SEQS || num_seqs >= 64 * kFlatSlots || max_seqlen_k <= 0)
+    return p;
+  const int64_t keys = (int64_t)num_seqs * max_seqlen_k;
+  if (keys < PK_DECODE_FLAT_MIN_KEYS || keys >= (1ll << 30) ||
+      max_seqlen_k <= decode_split_tokens(num_seqs, max_seqlen_k))
+    return p;
+  int min_chunk = PK_DECODE_FLAT_MIN_CHUNK;
+  const int need = (max_seqlen_k + kCombineMaxSplits - 3) / (kCombineMaxSplits - 2);
+  if (min_chunk < need) min_chunk = (need + 7) / 8 * 8;
+  const int64_t groups = std::min<int64_t>(std::max(PK_DECODE_FLAT_GROUPS - num_seqs, 2),
+                                           (keys + min_chunk - 1) / min_chunk);
+  if (groups < 2) return p;
+  p.groups = (int)groups;
+  p.min_chunk = min_chunk;
+  return p;
+}
+
+hipError_t launch_decode(const AttnArgs& args, int group, bool paged, int max_seqlen_k,
                          hipStream_t stream) {
-  if (a.num_seqs <= 0 || max_seqlen_k <= 0) return hipSuccess;
+  if (args.num_seqs <= 0 || max_seqlen_k <= 0) return hipSuccess;
+  AttnArgs a = args;
+  a.flat_step = decode_step_keys(group);
   hipError_t err;
   switch (group) {
-    case 1: err = launch_decode_g<1, PK_DECODE_STEP_G2>(a, paged, stream); break;
-    case 2: err = launch_decode_g<2, PK_DECODE_STEP_G2>(a, paged, stream); break;
-    case 4: err = launch_decode_g<4, 4>(a, paged, stream); break;
-    case 8: err = launch_decode_g<8, 4>(a, paged, stream); break;
+    case 1: err = launch_decode_g<1, decode_step_keys(1)>(a, paged, stream); break;
+    case 2: err = launch_decode_g<2, decode_step_keys(2)>(a, paged, stream); break;
+    case 4: err = launch_decode_g<4, decode_step_keys(4)>(a, paged, stream); break;
+    case 8: err = launch_decode_g<8, decode_step_keys(8)>(a, paged, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;
-  if (a.max_splits > 1) {
+  if (a.max_splits > 1 || a.flat_groups > 0) {
     hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)a.num_heads, (unsigned)a.num_seqs),
                        dim3(kCombineThreads), 0, stream, a);
     err = hipGetLastError();
