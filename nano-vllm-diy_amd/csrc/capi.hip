@@ -58,9 +58,10 @@ struct WorkspaceLayout {
 };
 
 // [decode: partial numerators | partial (max, sum) | flat-grid record | shared-prefix plan]
-// (empty when no sequence can have more than one split: those write their output directly;
-// the partial regions hold the split grid's num_seqs x max_splits units or the flat grid's
-// num_seqs + groups, whichever is larger)
+// (empty when no sequence can have more than one split: those write their output directly).
+// Partial units: the split grid's num_seqs x max_splits (shared-prefix chunks in the first
+// slots of each sequence); with the flat grid, the shared-prefix chunks (num_seqs x
+// prefix_slots <= num_seqs x max_splits) followed by the grid's num_seqs + groups pieces.
 // [prefill: queue header | work items | merge list | partial numerators | (max, sum)]
 WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int max_seqlen_q, int max_seqlen_k) {
   WorkspaceLayout w{};
@@ -69,15 +70,15 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
   w.flat = pk::decode_flat_plan(num_seqs, max_seqlen_k);  // groups > 0 only when max_splits > 1
   if (w.max_splits > 1) {  // single-split sequences write their output directly
     size_t seq_units = (size_t)num_seqs * (size_t)w.max_splits;
-    if (w.flat.groups > 0) seq_units = std::max(seq_units, (size_t)num_seqs + (size_t)w.flat.groups);
+    if (w.flat.groups > 0) seq_units += (size_t)num_seqs + (size_t)w.flat.groups;
     const size_t units = seq_units * (size_t)num_heads;
     w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
     w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
   }
   size_t off = w.part_o_bytes + w.part_ml_bytes;
-  if (w.flat.groups > 0) {  // the run length the flat grid used, for the combine
+  if (w.flat.groups > 0) {  // the flat grid's run length and key-line positions, for the combine
     w.flat_meta_off = off;
-    off += kWorkspaceAlign;
+    off += round_up(((size_t)num_seqs + 2) * sizeof(int32_t), kWorkspaceAlign);
   }
   if (w.max_splits > 1) {  // the shared-prefix plan: at most one item per (sequence, slot)
     w.sp_plan_off = off;
@@ -365,6 +366,7 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   a.max_splits = ws.max_splits > 0 ? ws.max_splits : 1;
   a.grid_splits = a.max_splits;
   a.prefix_chunk = 1;
+  a.prefix_stride = a.max_splits;
   if (shared_prefix_keys > 0 && paged && !fp && ws.max_splits > 1 && num_seqs <= pk::kSharedPrefixMaxSeqs) {
     // Shared-prefix decode. Chunks of CK = lcm(block_size, split) keys and a prefix of a
     // whole number of chunks keep the partial slots within the workspace's: P / CK prefix
@@ -388,10 +390,14 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
     a.part_o = reinterpret_cast<float*>(wsb);
     a.part_ml = reinterpret_cast<float*>(wsb + ws.part_o_bytes);
   }
-  if (a.prefix_keys == 0 && ws.flat.groups > 0) {  // the flat decode grid (the shared-prefix path splits)
+  if (ws.flat.groups > 0) {  // the flat decode grid: pieces after the shared-prefix chunks, if any
     a.flat_groups = ws.flat.groups;
     a.flat_min_chunk = ws.flat.min_chunk;
     a.flat_meta = reinterpret_cast<int32_t*>(wsb + ws.flat_meta_off);
+    if (a.prefix_keys > 0) {
+      a.prefix_stride = a.prefix_slots;
+      a.flat_unit0 = num_seqs * a.prefix_slots;
+    }
   }
   if (max_seqlen_q > 1) {
     a.pf_queue = reinterpret_cast<int32_t*>(wsb + ws.pf_queue_off);

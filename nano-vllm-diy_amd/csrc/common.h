@@ -47,23 +47,28 @@ struct AttnArgs {
   int32_t split_tokens;
   int32_t max_splits;           // partial slots per sequence (stride of part_o / part_ml)
   int32_t grid_splits;          // splits the decode grid covers per sequence
-  // Flat decode grid (flat_groups > 0, no shared prefix): work-group w takes the keys at
-  // positions [w * chunk, (w + 1) * chunk) of the batch's key line (key t of sequence b at
-  // cu_k[b] + t); a sequence's piece in work-group w is partial unit b + w
-  // (part_o: [num_seqs + flat_groups][num_heads][head_dim]). chunk >= flat_min_chunk is set
-  // on the device from the largest cu_k entry and kept in flat_meta[0] for the combine;
-  // flat_step = keys per pipeline step (set by the decode launch).
+  // Flat decode grid (flat_groups > 0): the decode keys of the batch -- per decode sequence
+  // b its keys after the shared prefix, c_b = Lk - min(prefix_keys, Lk) of them -- laid end
+  // to end in sequence order (the key line: sequence b from position pos_b = c_0 + ... +
+  // c_{b-1}) and cut into flat_groups runs of `chunk` keys; the piece of sequence b in run w
+  // is work-group b + w and partial unit flat_unit0 + b + w. chunk >= flat_min_chunk is set
+  // on the device; flat_meta holds chunk, then pos_b, for the combine. flat_step = keys per
+  // pipeline step (set by the decode launch).
   int32_t flat_groups;
   int32_t flat_min_chunk;
   int32_t flat_step;
+  int32_t flat_unit0;
   int32_t* flat_meta;
   // Shared-prefix decode: keys [0, min(prefix_keys, Lk)) of a decode sequence are computed by
   // the shared-prefix kernel, one partial per chunk of prefix_chunk keys in slots
-  // [0, prefix_slots); the split kernel covers the keys after them, its split s in slot
-  // prefix_slots + s. prefix_keys == 0 (prefix_chunk 1, prefix_slots 0): off.
+  // [0, prefix_slots); the decode kernel covers the keys after them (split grid: its split s
+  // in slot prefix_slots + s; flat grid: its pieces). prefix_keys == 0 (prefix_chunk 1,
+  // prefix_slots 0): off.
   int32_t prefix_keys;
   int32_t prefix_chunk;
   int32_t prefix_slots;
+  int32_t prefix_stride;        // partial units per sequence of the prefix chunk partials (chunk j of
+                                // sequence b at unit b * prefix_stride + j)
   // Shared-prefix plan (workspace, after the decode partials): item counts per chunk
   // (kSharedPrefixHeaderInts), then items [prefix_slots][num_seqs] of two int4 ((first member,
   // members, keys held, 0), (block ids of the chunk)), then members [prefix_slots][num_seqs]

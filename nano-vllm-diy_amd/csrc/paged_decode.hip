@@ -466,30 +466,36 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
                                   ((int64_t)b * a.max_splits + slot) * a.num_heads);
 }
 
-// Maximum of a non-negative int over the wavefront, in a scalar register.
-__device__ __forceinline__ int wave_max_nonneg(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppXor1, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppXor2, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppHalfMirror, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(0, v, kDppMirror, 0xf, 0xf, false));
-  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+// Inclusive sum over the wavefront: lane i gets x_0 + ... + x_i. DPP row shifts scan each
+// 16-lane row, then the totals of the rows below are added (three readlanes).
+__device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1 (row lane 0 adds 0)
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
-// Flat mode: the batch's keys, at the positions cu_seqlens_k gives them (key t of sequence b
-// at cu_k[b] + t), are cut into W = flat_groups runs of `chunk` keys, so that the work is
-// spread evenly whatever the length mix (the split grid gives each sequence whole splits:
-// its last split is ragged, and short sequences leave many work-groups empty). A pipeline
-// step (U keys at a multiple of U inside its sequence) belongs to the run holding its first
-// key, so sequence b has a piece in runs w0(b) .. w1(b) (the runs of its first and last
-// steps). Piece (b, w) is work-group u = b + w and partial unit u: the index is unique
-// because both the runs and the sequences tile the key line in order, so
-// b + w1(b) < b' + w0(b') for b < b'. The grid has W + num_seqs work-groups; those whose
-// index falls between two sequences' ranges exit at once.
-// chunk = max(flat_min_chunk, ceil(T / W) rounded up to U), T = the largest cu_seqlens_k
-// entry (graph padding zeroes trailing entries, so the last one need not be the total);
-// work-group 0 records it for the combine. One wavefront holds every sequence's bounds
-// (num_seqs < 64 * kFlatSlots) and finds the work-group's sequence with one ballot per slot.
+// Flat mode: the decode keys of the batch -- per decode sequence b the c_b keys after its
+// shared prefix (all of them without one) -- are laid end to end in sequence order (the key
+// line: sequence b from position pos_b = c_0 + ... + c_{b-1}) and cut into W = flat_groups
+// runs of `chunk` keys, so that every work-group streams the same number of K/V rows
+// whatever the length mix (the split grid gives each sequence whole splits: its last split
+// is ragged, short sequences leave many work-groups empty, and prefill rows of a mixed batch
+// or keys past max_seqlen_k take no place on the line). A pipeline step (U keys at a multiple
+// of U after the prefix) belongs to the run holding its first key, so sequence b has a piece
+// in runs w0(b) .. w1(b) (the runs of its first and last steps). Piece (b, w) is work-group
+// u = b + w and partial unit flat_unit0 + u: the index is unique because the runs and the
+// sequences both tile the line in order, so b + w1(b) < b' + w0(b') for b < b'. The grid has
+// W + num_seqs + 1 work-groups: those whose index falls between two sequences' ranges exit at
+// once, and the last one records chunk and every pos_b for the combine. (174 VGPRs for G = 2,
+// two wavefronts per SIMD: the 1024-work-group grid of two-wavefront groups fits 4 per CU.)
+// chunk = max(flat_min_chunk, ceil(T / W) rounded up to U), T = the line's length. One
+// wavefront holds every sequence's bounds (num_seqs < 64 * kFlatSlots), forms the line with a
+// wavefront prefix sum and finds the work-group's sequence with one ballot per slot.
 constexpr int kFlatSlots = 8;
 
 template <int G, int U, bool PAGED, bool FUSED>
@@ -498,62 +504,70 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(con
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;
   const int n = a.num_seqs;
-  // lane l, slot s: sequence e = l + 64 s (bounds of both its key and query ranges)
-  int kb[kFlatSlots], ke[kFlatSlots], qb[kFlatSlots], qe[kFlatSlots];
+  // lane l, slot s: sequence e = l + 64 s
+  int kb[kFlatSlots], qb[kFlatSlots], lk[kFlatSlots], cnt[kFlatSlots], pos[kFlatSlots];
   int T = 0;
 #pragma unroll
   for (int s = 0; s < kFlatSlots; ++s) {
-    kb[s] = ke[s] = qb[s] = qe[s] = 0;
-    if (64 * s <= n) {
+    kb[s] = qb[s] = lk[s] = cnt[s] = pos[s] = 0;
+    if (64 * s < n) {
       const int e = lane + 64 * s;
-      if (e <= n) kb[s] = a.cu_k[e];
       if (e < n) {
-        ke[s] = a.cu_k[e + 1];
+        kb[s] = a.cu_k[e];
         qb[s] = a.cu_q[e];
-        qe[s] = a.cu_q[e + 1];
+        const int k1 = a.cu_k[e + 1], q1 = a.cu_q[e + 1];
+        lk[s] = min(k1 - kb[s], a.max_seqlen_k);
+        const int pb = max(0, min(a.prefix_keys, lk[s]));
+        cnt[s] = (q1 - qb[s] == 1 && lk[s] > 0) ? lk[s] - pb : 0;  // decode keys after the prefix
       }
-      T = max(T, kb[s]);
+      const int incl = wave_inclusive_sum(cnt[s], lane);
+      pos[s] = T + incl - cnt[s];
+      T += __builtin_amdgcn_readlane(incl, kWave - 1);
     }
   }
-  T = wave_max_nonneg(T);
-  const int per = (int)(((int64_t)T + a.flat_groups - 1) / a.flat_groups);
+  const int per = (T + a.flat_groups - 1) / a.flat_groups;
   const int chunk = max(a.flat_min_chunk, (per + U - 1) / U * U);
   const int u = blockIdx.x;
-  // the decode sequence (Lq == 1, Lk > 0) with b + w0(b) <= u <= b + w1(b), if any
-  int b = -1, q0 = 0, k0 = 0, Lk = 0;
+  // the decode sequence with b + w0(b) <= u <= b + w1(b), if any
+  int b = -1, q0 = 0, k0 = 0, Lk = 0, p0 = 0, cb = 0;
 #pragma unroll
   for (int s = 0; s < kFlatSlots; ++s) {
     if (64 * s < n) {
       const int e = lane + 64 * s;
-      const int lk = min(ke[s] - kb[s], a.max_seqlen_k);
-      const bool dec = e < n && qe[s] - qb[s] == 1 && lk > 0 && kb[s] >= 0;
-      const int w0 = kb[s] / chunk;
-      const int w1 = (int)(((int64_t)kb[s] + (lk - 1) / U * U) / chunk);
-      const uint64_t m = __builtin_amdgcn_ballot_w64(dec && e + w0 <= u && u <= e + w1);
+      const int w0 = pos[s] / chunk;
+      const int w1 = (pos[s] + (cnt[s] - 1) / U * U) / chunk;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(cnt[s] > 0 && e + w0 <= u && u <= e + w1);
       if (m) {
         const int j = __builtin_ctzll(m);
         b = 64 * s + j;
         q0 = __builtin_amdgcn_readlane(qb[s], j);
         k0 = __builtin_amdgcn_readlane(kb[s], j);
-        Lk = __builtin_amdgcn_readlane(lk, j);
+        Lk = __builtin_amdgcn_readlane(lk[s], j);
+        p0 = __builtin_amdgcn_readlane(pos[s], j);
+        cb = __builtin_amdgcn_readlane(cnt[s], j);
       }
     }
   }
-  // The record is written after the unit, so that no global store precedes its block-table
-  // reads: the compiler then knows the table unchanged and reads it with scalar loads.
-  const bool recorder = blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0;
   if (b < 0) {
-    if (recorder) a.flat_meta[0] = chunk;
+    // The last work-group holds no piece (b + w1(b) <= num_seqs - 1 + W - 1): it records the
+    // line for the combine. (Recorded here, after the search, so that its stores precede no
+    // block-table read on any path: the compiler then reads the table with scalar loads.)
+    if (u == a.flat_groups + n && blockIdx.y == 0 && wave == 0) {
+      if (lane == 0) a.flat_meta[0] = chunk;
+#pragma unroll
+      for (int s = 0; s < kFlatSlots; ++s)
+        if (lane + 64 * s < n) a.flat_meta[1 + lane + 64 * s] = pos[s];
+    }
     return;
   }
-  const int64_t F0 = (int64_t)(u - b) * chunk, F1 = F0 + chunk;  // this run's keys
-  const int64_t d = F0 - k0;
-  const int t_begin = d > 0 ? (int)((d + U - 1) / U * U) : 0;
-  const int t_end = (int)min<int64_t>(Lk, (F1 - k0 + U - 1) / U * U);
-  // the sequence's first and last steps in one run: this piece is all of it
-  const bool direct = k0 / chunk == ((int64_t)k0 + (Lk - 1) / U * U) / chunk;
-  decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct, (int64_t)u * a.num_heads);
-  if (recorder) a.flat_meta[0] = chunk;
+  const int Pb = Lk - cb;                                // keys of the shared prefix
+  const int F0 = (u - b) * chunk, F1 = F0 + chunk;       // this run, on the line
+  const int t_begin = Pb + (F0 > p0 ? (F0 - p0 + U - 1) / U * U : 0);
+  const int t_end = min(Lk, Pb + (F1 - p0 + U - 1) / U * U);
+  // the sequence's first and last steps in one run and no prefix partial: this piece is all of it
+  const bool direct = Pb == 0 && p0 / chunk == (p0 + (cb - 1) / U * U) / chunk;
+  decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
+                                  ((int64_t)a.flat_unit0 + u) * a.num_heads);
 }
 
 // Merge the per-split partials of one (sequence, head). A separate launch (rather than a
@@ -602,31 +616,33 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
   if (Lk <= 0) return;
   const int H = a.num_heads;
-  int npre, nsplit, gap;
-  int64_t unit0;  // partial j of (sequence, head) at unit unit0 + slot_of(j) H
+  // partial j of the sequence: its prefix chunks j < npre (units pre0 + j), then the decode
+  // kernel's splits or pieces (units post0 + j)
+  const int Pb = min(a.prefix_keys, Lk);
+  const int npre = (Pb + a.prefix_chunk - 1) / a.prefix_chunk;
+  int nsplit;
+  int64_t pre0 = (int64_t)b * a.prefix_stride, post0;
   if (a.flat_groups > 0) {
-    // flat mode: the pieces of work-groups w0 .. w1 (those holding the first and the last
-    // step's first key), piece of work-group w at unit b + w
-    const int64_t chunk = a.flat_meta[0];
-    const int64_t w0 = max(0, k_lo) / chunk;
-    const int64_t w1 = ((int64_t)k_lo + (Lk - 1) / a.flat_step * a.flat_step) / chunk;
-    npre = 0;
-    gap = 0;
-    nsplit = (int)min<int64_t>(w1 - w0 + 1, kCombineMaxSplits);  // the plan keeps it <= kCombineMaxSplits
-    if (nsplit <= 1) return;  // written directly by the split kernel
-    unit0 = ((int64_t)b + w0) * H + h;
+    // flat grid: the pieces of runs w0 .. w1 (those holding the first and the last step of the
+    // sequence's keys after the prefix, on the key line), piece of run w at unit flat_unit0 + b + w
+    const int cb = Lk - Pb;
+    int64_t w0 = 0, w1 = -1;
+    if (cb > 0) {
+      const int64_t chunk = a.flat_meta[0], p0 = a.flat_meta[1 + b];
+      w0 = p0 / chunk;
+      w1 = (p0 + (cb - 1) / a.flat_step * a.flat_step) / chunk;
+    }
+    nsplit = npre + (int)(w1 - w0 + 1);
+    post0 = a.flat_unit0 + b + w0 - npre;
   } else {
-    // partial j < npre: prefix chunk j (slot j); the others: split j - npre (slot prefix_slots + j - npre)
-    const int Pb = min(a.prefix_keys, Lk);
-    npre = (Pb + a.prefix_chunk - 1) / a.prefix_chunk;
     nsplit = npre + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
-    if (nsplit <= 1 && npre == 0) return;  // written directly by the split kernel
-    gap = a.prefix_slots - npre;
-    unit0 = (int64_t)b * a.max_splits * H + h;
+    post0 = (int64_t)b * a.max_splits + a.prefix_slots - npre;
   }
-  const auto slot_of = [&](int j) { return j < npre ? j : j + gap; };
+  if (nsplit <= 1 && npre == 0) return;  // written directly by the decode kernel
+  nsplit = min(nsplit, kCombineMaxSplits);  // the launch keeps it within (the weight table's size)
+  const auto unit_of = [&](int j) -> int64_t { return j < npre ? pre0 + j : post0 + j; };
   const int d = threadIdx.x;
-  const float* po = a.part_o + unit0 * D + partial_slot(d);
+  const float* po = a.part_o + (int64_t)h * D + partial_slot(d);
   const int64_t stride = (int64_t)H * D;
   if (nsplit <= kCombineFast) {
     // Every load of the merge is issued at once: lane j < nsplit of each wavefront reads
@@ -636,10 +652,10 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
     // every lane by a readlane: no LDS permutes on the dependency chain.
     const int lane = threadIdx.x & (kWave - 1);
     float2 ml = make_float2(-INFINITY, 0.f);
-    if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)slot_of(lane) * H) * 2);
+    if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(lane) * H + h) * 2);
     float v[kCombineFast];
 #pragma unroll
-    for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[(int64_t)slot_of(j) * stride] : 0.f;
+    for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[unit_of(j) * stride] : 0.f;
     const float rm = row16_max(ml.x);
     const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
     const float w = lane < nsplit ? exp2_fast(ml.x - mx) : 0.f;
@@ -655,11 +671,11 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   // forms the weighted sum of element d with four independent accumulators.
   float mx = -INFINITY;
   for (int j = threadIdx.x; j < nsplit; j += kCombineThreads)
-    mx = fmaxf(mx, a.part_ml[(unit0 + (int64_t)slot_of(j) * H) * 2]);
+    mx = fmaxf(mx, a.part_ml[(unit_of(j) * H + h) * 2]);
   mx = block_reduce(mx, true, red);
   float lsum = 0.f;
   for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit0 + (int64_t)slot_of(j) * H) * 2);
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(j) * H + h) * 2);
     const float w = exp2_fast(ml.x - mx);
     w_s[j] = w;
     lsum = fmaf(w, ml.y, lsum);
@@ -668,19 +684,19 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
   int j = 0;
   for (; j + 4 <= nsplit; j += 4) {
-    o0 = fmaf(w_s[j], po[(int64_t)slot_of(j) * stride], o0);
-    o1 = fmaf(w_s[j + 1], po[(int64_t)slot_of(j + 1) * stride], o1);
-    o2 = fmaf(w_s[j + 2], po[(int64_t)slot_of(j + 2) * stride], o2);
-    o3 = fmaf(w_s[j + 3], po[(int64_t)slot_of(j + 3) * stride], o3);
+    o0 = fmaf(w_s[j], po[unit_of(j) * stride], o0);
+    o1 = fmaf(w_s[j + 1], po[unit_of(j + 1) * stride], o1);
+    o2 = fmaf(w_s[j + 2], po[unit_of(j + 2) * stride], o2);
+    o3 = fmaf(w_s[j + 3], po[unit_of(j + 3) * stride], o3);
   }
-  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], po[(int64_t)slot_of(j) * stride], o0);
+  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], po[unit_of(j) * stride], o0);
   a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(((o0 + o1) + (o2 + o3)) / lsum);
 }
 
 template <int G, int U>
 hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const bool flat = a.flat_groups > 0;
-  const int64_t units = flat ? (int64_t)a.num_seqs + a.flat_groups : (int64_t)a.num_seqs * a.max_splits;
+  const int64_t units = flat ? (int64_t)a.num_seqs + a.flat_groups : (int64_t)a.num_seqs * a.max_splits;  // decode kernel's
   a.store_through = units * a.num_heads * kHeadDim * 4 > kStoreThroughBytes;
   const int quads = (a.num_kv_heads + 3) / 4;   // wavefronts needed for all kv heads
   int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
@@ -689,7 +705,7 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const dim3 block((unsigned)(waves * kWave));
   const bool fused = a.qkv != nullptr || a.new_k != nullptr;  // paged only (checked by their entry points)
   if (flat) {
-    const dim3 grid((unsigned)(a.flat_groups + a.num_seqs), (unsigned)zgroups);
+    const dim3 grid((unsigned)(a.flat_groups + a.num_seqs + 1), (unsigned)zgroups);  // + the recorder
     if (fused)
       hipLaunchKernelGGL((decode_flat_kernel<G, U, true, true>), grid, block, 0, stream, a);
     else if (paged)

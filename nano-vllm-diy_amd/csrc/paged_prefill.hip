@@ -1088,12 +1088,12 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
       }
     }
 
-    // partial of (member, head h) in slot c, in the decode split kernel's layout: numerator
+    // partial of (member, head h) for chunk c, in the decode kernel's layout: numerator
     // element d at partial slot (d & 4 ? 64 : 0) + 4 (d >> 3) + (d & 3); O^T element rr of
     // d-block md is d = 32 md + 8 (rr >> 2) + 4 half + (rr & 3), i.e. four consecutive slots
     const float l_tot = swap_halves_sum(l_i[0]);
     if (active && mem < nmem) {
-      const int64_t unit = ((int64_t)seq * a.max_splits + c) * a.num_heads + h;
+      const int64_t unit = ((int64_t)seq * a.prefix_stride + c) * a.num_heads + h;
       float* po = a.part_o + unit * D + 64 * half;
 #pragma unroll
       for (int md = 0; md < 4; ++md)

@@ -85,12 +85,14 @@ def test_workspace_size_formula():
     # item (32 B) and one member (8 B)
     want += math.ceil((1024 + 256 * (8192 // split) * 40) / 256) * 256
     assert ws == want
-    # 128 sequences of <= 2048 keys take the flat decode grid (1024 work-groups: 896 runs of
-    # keys + 128 sequences, one partial unit each, fewer than the split grid's 128 x 16 units
-    # of 128-key splits), which adds one 256-byte line recording its run length
+    # 128 sequences of <= 2048 keys take the flat decode grid: 896 runs of keys + 128
+    # sequences, one partial unit each, after room for shared-prefix chunks (at most the split
+    # grid's 128 x 16 units of 128-key splits), and a record of the run length and the 128
+    # key-line positions (130 ints in 256-byte lines)
     ws = lib.pk_varlen_attention_workspace_bytes(128, HQ, HEAD_DIM, 1, 2048)
-    units = 128 * (2048 // 128) * HQ
-    want = math.ceil(units * HEAD_DIM * 4 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256 + 256
+    units = (128 * (2048 // 128) + 128 + 896) * HQ
+    want = math.ceil(units * HEAD_DIM * 4 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
+    want += math.ceil(130 * 4 / 256) * 256
     want += math.ceil((1024 + 128 * (2048 // 128) * 40) / 256) * 256
     assert ws == want
 
