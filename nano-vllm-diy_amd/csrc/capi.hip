@@ -72,7 +72,7 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
     size_t seq_units = (size_t)num_seqs * (size_t)w.max_splits;
     if (w.flat.groups > 0) seq_units += (size_t)num_seqs + (size_t)w.flat.groups;
     const size_t units = seq_units * (size_t)num_heads;
-    w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(float), kWorkspaceAlign);
+    w.part_o_bytes = round_up(units * (size_t)head_dim * sizeof(uint16_t), kWorkspaceAlign);  // bf16
     w.part_ml_bytes = round_up(units * 2 * sizeof(float), kWorkspaceAlign);
   }
   size_t off = w.part_o_bytes + w.part_ml_bytes;
@@ -387,7 +387,7 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   }
   char* const wsb = static_cast<char*>(workspace);
   if (ws.part_o_bytes > 0) {
-    a.part_o = reinterpret_cast<float*>(wsb);
+    a.part_o = reinterpret_cast<uint16_t*>(wsb);
     a.part_ml = reinterpret_cast<float*>(wsb + ws.part_o_bytes);
   }
   if (ws.flat.groups > 0) {  // the flat decode grid: pieces after the shared-prefix chunks, if any

@@ -40,13 +40,15 @@ struct AttnArgs {
   uint16_t* out;
   int64_t out_row_stride;
   // split-K decode scratch (workspace)
-  float* part_o;                // [num_seqs][max_splits][num_heads][head_dim]
-  float* part_ml;               // [num_seqs][max_splits][num_heads][2] = (max, sum)
+  uint16_t* part_o;             // [unit][num_heads][head_dim] bf16: the unit's normalised output o / l
+  float* part_ml;               // [unit][num_heads][2] = (max in the exp2 domain, sum)
   int32_t stream_from;           // decode splits starting at key >= this use non-temporal loads (< 0: none)
   int32_t store_through;         // decode partials written through L2 (set by the decode launch)
   int32_t split_tokens;
   int32_t max_splits;           // partial slots per sequence (stride of part_o / part_ml)
   int32_t grid_splits;          // splits the decode grid covers per sequence
+  int32_t decode_ks;            // key sub-ranges (wavefronts) per split, set by the decode launch
+  int32_t decode_wq;            // kv-head quads (wavefronts) per sub-range, set by the decode launch
   // Flat decode grid (flat_groups > 0): the decode keys of the batch -- per decode sequence
   // b its keys after the shared prefix, c_b = Lk - min(prefix_keys, Lk) of them -- laid end
   // to end in sequence order (the key line: sequence b from position pos_b = c_0 + ... +
@@ -138,6 +140,7 @@ inline int64_t prefill_item_cap(int num_seqs, int num_heads, int max_seqlen_q) {
          kPrefillPartCap;
 }
 
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

@@ -68,6 +68,15 @@ namespace {
 #endif
 
 constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
+// Small split grids give each split several wavefronts over sub-ranges of its keys (decode_unit):
+// up to PK_DECODE_SUB_RANGES of them while the grid stays under PK_DECODE_SUB_WAVES wavefronts.
+#ifndef PK_DECODE_SUB_RANGES
+#define PK_DECODE_SUB_RANGES 2   // 8 sequences of 256-2048 keys: 1 / 2 / 4 sub-ranges 18.6 / 18.0 / 19.4 us
+#endif
+#ifndef PK_DECODE_SUB_WAVES
+#define PK_DECODE_SUB_WAVES 4096
+#endif
+constexpr int kDecodeMaxSplitWaves = 8;  // wavefronts of a split work-group (quads x sub-ranges)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -82,19 +91,13 @@ constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through
 // bound, 114 -> 117 us; 128 sequences of 512-4096 keys, 221 -> 226 us).
 constexpr int64_t kStoreThroughBytes = 24ll << 20;
 
-// Slot of head_dim element d in a head's partial numerator row: lane c of the split kernel
-// holds elements 8c .. 8c + 7 and writes 8c .. 8c + 3 to slots 4c .. 4c + 3 and 8c + 4 ..
-// 8c + 7 to slots 64 + 4c .., so each of its two 16-byte stores covers 256 contiguous bytes
-// per head row. (Element order 8c .. 8c + 7 at slot 8c would leave every store instruction
-// writing every other 16 bytes: written through L2 that doubles the bytes that reach HBM.)
-__device__ __forceinline__ int partial_slot(int d) { return (d & 4 ? kHeadDim / 2 : 0) + (d >> 3) * 4 + (d & 3); }
-
+// A unit's partial: its normalised output o / l in bf16 (as precise as an unsplit row's
+// output, and half the bytes of fp32 numerators: writes that land in the middle of the K/V
+// read stream cost far more than reads) and (max in the exp2 domain, sum) in fp32.
 template <int AUX>
 __device__ __forceinline__ void store_partial(const __amdgpu_buffer_rsrc_t& po_rs, const __amdgpu_buffer_rsrc_t& pml_rs,
-                                              int o, int ml_off, const f32x4& lo, const f32x4& hi, const f32x2& ml,
-                                              bool with_ml) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), po_rs, o, 0, AUX);
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), po_rs, o + kHeadDim * 2, 0, AUX);
+                                              int o, int ml_off, const uint4& w, const f32x2& ml, bool with_ml) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), po_rs, o, 0, AUX);
   if (with_ml) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, ml), pml_rs, ml_off, 0, AUX);
 }
 
@@ -341,15 +344,32 @@ __device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>
   }
 }
 
+// Softmax state floats per lane that a sub-range wavefront hands over in LDS: (m, l) and the
+// 8 numerator elements of each of the G heads.
+template <int G>
+constexpr int kSubStateFloats = G * 10;
+
 // One work unit: keys [t_begin, t_end) of decode sequence b (query row q0, keys from k0 in
 // flat mode, Lk keys in all) for the kv heads of this wavefront. direct: the unit holds every
 // key of the sequence, so it normalises and writes the output row itself; otherwise it
 // leaves its (max, sum, numerator) partial at partial unit unit0 (x num_heads) for the combine.
+// With a.decode_ks > 1 (small split grids) the unit's keys are cut into decode_ks sub-ranges
+// of whole pipeline steps, one per wavefront (sub = 0 .. decode_ks - 1, same kv heads): each
+// streams its own keys, the others hand their softmax state to sub-range 0 through LDS
+// (sub_lds: [decode_ks - 1][decode_wq][kSubStateFloats][64] floats) and it merges them and
+// stores, so a unit keeps one partial while more loads are in flight.
 template <int G, int U, bool PAGED, bool FUSED>
 __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_first, int b, int q0, int k0, int Lk,
-                                            int t_begin, int t_end, bool direct, int64_t unit0) {
+                                            int t_begin, int t_end, bool direct, int64_t unit0, int sub = 0,
+                                            int qw = 0, float* sub_lds = nullptr) {
   static_assert(U % 2 == 0, "P.V pairs keys");
   constexpr int D = kHeadDim;
+  const int ks = a.decode_ks;
+  if (ks > 1) {  // this wavefront's whole steps of the unit
+    const int per = ((t_end - t_begin + U - 1) / U + ks - 1) / ks * U;
+    t_begin = min(t_end, t_begin + sub * per);
+    t_end = min(t_end, t_begin + per);
+  }
   const int c = lane & 15;
   const int g_lane = g_first + (lane >> 4);               // this DPP row's kv head
   const bool row_live = g_lane < a.num_kv_heads;
@@ -392,7 +412,9 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
   // those are the reads worth keeping in L2 / Infinity Cache; everything past them is read
   // once per step and only displaces useful lines. Decided per split (by its first key).
   const bool stream = a.stream_from >= 0 && t_begin >= a.stream_from;
-  if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
+  if (t_begin >= t_end) {
+    // an empty sub-range (its unit has fewer steps than sub-ranges): state stays (-inf, 0, 0)
+  } else if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
     fused_producer<G>(a, st, q0, g, c, row_live, true);
     if (stream)
       decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, nothing);
@@ -404,31 +426,60 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
     decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
   }
 
+  if (ks > 1) {  // merge the sub-ranges' states into sub-range 0 (every wavefront reaches the barrier)
+    constexpr int F = kSubStateFloats<G>;
+    if (sub > 0) {
+      float* dst = sub_lds + ((size_t)((sub - 1) * a.decode_wq + qw) * F) * kWave + lane;
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        dst[(10 * i) * kWave] = st.m[i];
+        dst[(10 * i + 1) * kWave] = st.l[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[(10 * i + 2 + e) * kWave] = st.acc[i][e];
+      }
+    }
+    __syncthreads();
+    if (sub > 0) return;
+    for (int r = 1; r < ks; ++r) {
+      const float* src = sub_lds + ((size_t)((r - 1) * a.decode_wq + qw) * F) * kWave + lane;
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const float mr = src[(10 * i) * kWave], lr = src[(10 * i + 1) * kWave];
+        const float mx = fmaxf(st.m[i], mr);
+        const float f0 = st.m[i] == -INFINITY ? 0.f : exp2_fast((st.m[i] - mx) * c2);
+        const float f1 = mr == -INFINITY ? 0.f : exp2_fast((mr - mx) * c2);
+        st.m[i] = mx;
+        st.l[i] = st.l[i] * f0 + lr * f1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.acc[i][e] = st.acc[i][e] * f0 + src[(10 * i + 2 + e) * kWave] * f1;
+      }
+    }
+  }
+
   if (!row_live) return;
-  // Partials of this unit: H heads x (D numerators, (max, sum)), contiguous, written
-  // through L2 or left in it by the launch's choice (kStoreThroughBytes).
-  const __amdgpu_buffer_rsrc_t po_rs = row_rsrc(a.part_o + unit0 * D, (uint32_t)(H * D * 4));
+  // Partials of this unit: H heads x (D outputs in bf16, (max, sum)), contiguous, written
+  // through L2 or left in it by the launch's choice (kStoreThroughBytes). A unit holds >= 1
+  // key, so l >= 1 (its largest score contributes exp2(0)).
+  const __amdgpu_buffer_rsrc_t po_rs = row_rsrc(a.part_o + unit0 * D, (uint32_t)(H * D * 2));
   const __amdgpu_buffer_rsrc_t pml_rs = row_rsrc(a.part_ml + unit0 * 2, (uint32_t)(H * 8));
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int h = g * G + i;
-    if (direct) {  // the only unit of this sequence: normalise and store
-      const float inv = 1.f / st.l[i];
-      uint4 w;
-      w.x = pack_bf16x2(st.acc[i][0] * inv, st.acc[i][1] * inv);
-      w.y = pack_bf16x2(st.acc[i][2] * inv, st.acc[i][3] * inv);
-      w.z = pack_bf16x2(st.acc[i][4] * inv, st.acc[i][5] * inv);
-      w.w = pack_bf16x2(st.acc[i][6] * inv, st.acc[i][7] * inv);
+    const float inv = 1.f / st.l[i];
+    uint4 w;
+    w.x = pack_bf16x2(st.acc[i][0] * inv, st.acc[i][1] * inv);
+    w.y = pack_bf16x2(st.acc[i][2] * inv, st.acc[i][3] * inv);
+    w.z = pack_bf16x2(st.acc[i][4] * inv, st.acc[i][5] * inv);
+    w.w = pack_bf16x2(st.acc[i][6] * inv, st.acc[i][7] * inv);
+    if (direct) {  // the only unit of this sequence: its output row
       *reinterpret_cast<uint4*>(a.out + (int64_t)q0 * a.out_row_stride + h * D + c * 8) = w;
     } else {
-      const int o = (h * D + c * 4) * 4;  // partial_slot(8c .. 8c + 3) = 4c: see partial_slot
-      const f32x4 lo = {st.acc[i][0], st.acc[i][1], st.acc[i][2], st.acc[i][3]};
-      const f32x4 hi = {st.acc[i][4], st.acc[i][5], st.acc[i][6], st.acc[i][7]};
+      const int o = (h * D + c * 8) * 2;  // 16 lanes store one 256-byte head row
       const f32x2 ml = {st.m[i] * c2, st.l[i]};  // merged in the exp2 domain: the scaled max
       if (a.store_through)
-        store_partial<kStoreThrough>(po_rs, pml_rs, o, h * 8, lo, hi, ml, c == 0);
+        store_partial<kStoreThrough>(po_rs, pml_rs, o, h * 8, w, ml, c == 0);
       else
-        store_partial<0>(po_rs, pml_rs, o, h * 8, lo, hi, ml, c == 0);
+        store_partial<0>(po_rs, pml_rs, o, h * 8, w, ml, c == 0);
     }
   }
 }
@@ -436,11 +487,14 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
 // Split mode: grid (splits x sequences, kv-head groups); a work-group takes split `split` of
 // one sequence (split_tokens keys after the shared prefix, if any).
 template <int G, int U, bool PAGED, bool FUSED>
-__global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(kWave* kDecodeMaxSplitWaves) void decode_split_kernel(const AttnArgs a) {
+  extern __shared__ float sub_lds[];  // sub-range states (decode_ks > 1)
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
-  // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
-  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
+  // wavefront = (sub-range, kv-head quad of the group); the launch divides the kv heads
+  // evenly over the quads: every wavefront has >= 1 live row
+  const int qw = wave % a.decode_wq, sub = wave / a.decode_wq;
+  const int g_first = (blockIdx.y * a.decode_wq + qw) * 4;  // first kv head of the wave
   // Work-groups are dispatched round-robin over the 8 XCDs in linear id order. Split-major
   // order with the sequence rotated by the split index sends consecutive splits of one
   // sequence to consecutive XCDs, so every XCD gets about 1/8 of each sequence whatever the
@@ -463,7 +517,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   const int nsplit = (Pb + a.prefix_chunk - 1) / a.prefix_chunk + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
   const int slot = a.prefix_slots + split;
   decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, nsplit == 1,
-                                  ((int64_t)b * a.max_splits + slot) * a.num_heads);
+                                  ((int64_t)b * a.max_splits + slot) * a.num_heads, sub, qw, sub_lds);
 }
 
 // Inclusive sum over the wavefront: lane i gets x_0 + ... + x_i. DPP row shifts scan each
@@ -612,6 +666,10 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   const int q1 = a.cu_q[b + 1];
   const int k_lo = a.cu_k[b];
   const int k_hi = a.cu_k[b + 1];
+  // the flat grid's record is read in the same round of loads as the bounds
+  const bool flat = a.flat_groups > 0;
+  const int f_chunk = flat ? a.flat_meta[0] : 1;
+  const int f_pos = flat ? a.flat_meta[1 + b] : 0;
   if (q1 - q0 != 1) return;
   const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
   if (Lk <= 0) return;
@@ -622,15 +680,14 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   const int npre = (Pb + a.prefix_chunk - 1) / a.prefix_chunk;
   int nsplit;
   int64_t pre0 = (int64_t)b * a.prefix_stride, post0;
-  if (a.flat_groups > 0) {
+  if (flat) {
     // flat grid: the pieces of runs w0 .. w1 (those holding the first and the last step of the
     // sequence's keys after the prefix, on the key line), piece of run w at unit flat_unit0 + b + w
     const int cb = Lk - Pb;
-    int64_t w0 = 0, w1 = -1;
+    int w0 = 0, w1 = -1;
     if (cb > 0) {
-      const int64_t chunk = a.flat_meta[0], p0 = a.flat_meta[1 + b];
-      w0 = p0 / chunk;
-      w1 = (p0 + (cb - 1) / a.flat_step * a.flat_step) / chunk;
+      w0 = f_pos / f_chunk;
+      w1 = (f_pos + (cb - 1) / a.flat_step * a.flat_step) / f_chunk;
     }
     nsplit = npre + (int)(w1 - w0 + 1);
     post0 = a.flat_unit0 + b + w0 - npre;
@@ -642,7 +699,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   nsplit = min(nsplit, kCombineMaxSplits);  // the launch keeps it within (the weight table's size)
   const auto unit_of = [&](int j) -> int64_t { return j < npre ? pre0 + j : post0 + j; };
   const int d = threadIdx.x;
-  const float* po = a.part_o + (int64_t)h * D + partial_slot(d);
+  const uint16_t* po = a.part_o + (int64_t)h * D + d;
   const int64_t stride = (int64_t)H * D;
   if (nsplit <= kCombineFast) {
     // Every load of the merge is issued at once: lane j < nsplit of each wavefront reads
@@ -655,11 +712,13 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
     if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(lane) * H + h) * 2);
     float v[kCombineFast];
 #pragma unroll
-    for (int j = 0; j < kCombineFast; ++j) v[j] = j < nsplit ? po[unit_of(j) * stride] : 0.f;
+    // branch-free: past nsplit the last partial is read again, and its weight there is 0
+    // (a conditional 16-bit load per split compiles to a branch and a wait per split)
+    for (int j = 0; j < kCombineFast; ++j) v[j] = bf16_to_f32(po[unit_of(min(j, nsplit - 1)) * stride]);
     const float rm = row16_max(ml.x);
     const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
-    const float w = lane < nsplit ? exp2_fast(ml.x - mx) : 0.f;
-    const float rs = row16_sum(w * ml.y);
+    const float w = lane < nsplit ? exp2_fast(ml.x - mx) * ml.y : 0.f;  // each partial's weight: its share of l
+    const float rs = row16_sum(w);
     const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
     float acc = 0.f;
 #pragma unroll
@@ -676,20 +735,20 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
   float lsum = 0.f;
   for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) {
     const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(j) * H + h) * 2);
-    const float w = exp2_fast(ml.x - mx);
+    const float w = exp2_fast(ml.x - mx) * ml.y;
     w_s[j] = w;
-    lsum = fmaf(w, ml.y, lsum);
+    lsum += w;
   }
   lsum = block_reduce(lsum, false, red);  // its barriers also publish w_s
   float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
   int j = 0;
   for (; j + 4 <= nsplit; j += 4) {
-    o0 = fmaf(w_s[j], po[unit_of(j) * stride], o0);
-    o1 = fmaf(w_s[j + 1], po[unit_of(j + 1) * stride], o1);
-    o2 = fmaf(w_s[j + 2], po[unit_of(j + 2) * stride], o2);
-    o3 = fmaf(w_s[j + 3], po[unit_of(j + 3) * stride], o3);
+    o0 = fmaf(w_s[j], bf16_to_f32(po[unit_of(j) * stride]), o0);
+    o1 = fmaf(w_s[j + 1], bf16_to_f32(po[unit_of(j + 1) * stride]), o1);
+    o2 = fmaf(w_s[j + 2], bf16_to_f32(po[unit_of(j + 2) * stride]), o2);
+    o3 = fmaf(w_s[j + 3], bf16_to_f32(po[unit_of(j + 3) * stride]), o3);
   }
-  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], po[unit_of(j) * stride], o0);
+  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], bf16_to_f32(po[unit_of(j) * stride]), o0);
   a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(((o0 + o1) + (o2 + o3)) / lsum);
 }
 
@@ -705,6 +764,8 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const dim3 block((unsigned)(waves * kWave));
   const bool fused = a.qkv != nullptr || a.new_k != nullptr;  // paged only (checked by their entry points)
   if (flat) {
+    a.decode_ks = 1;  // one wavefront per kv-head quad and piece
+    a.decode_wq = waves;
     const dim3 grid((unsigned)(a.flat_groups + a.num_seqs + 1), (unsigned)zgroups);  // + the recorder
     if (fused)
       hipLaunchKernelGGL((decode_flat_kernel<G, U, true, true>), grid, block, 0, stream, a);
@@ -715,13 +776,23 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
     return hipGetLastError();
   }
   if (a.grid_splits <= 0) return hipSuccess;  // every decode key lies in the shared prefix
+  const int64_t groups = (int64_t)a.grid_splits * a.num_seqs * zgroups;
+  // sub-ranges: while the grid is small and each sub-range keeps >= 2 pipeline steps
+  int ks = 1;
+  while (ks < PK_DECODE_SUB_RANGES && waves * 2 * ks <= kDecodeMaxSplitWaves &&
+         groups * waves * 2 * ks <= PK_DECODE_SUB_WAVES && a.split_tokens >= 2 * ks * 2 * U)
+    ks *= 2;
+  a.decode_ks = ks;
+  a.decode_wq = waves;
   const dim3 grid((unsigned)(a.grid_splits * a.num_seqs), (unsigned)zgroups);
+  const dim3 sblock((unsigned)(waves * ks * kWave));
+  const size_t lds = ks > 1 ? (size_t)(ks - 1) * waves * kSubStateFloats<G> * kWave * sizeof(float) : 0;
   if (fused)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, sblock, lds, stream, a);
   else if (paged)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, sblock, lds, stream, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, sblock, lds, stream, a);
   return hipGetLastError();
 }
 

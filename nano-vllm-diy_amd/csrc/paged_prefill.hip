@@ -1088,19 +1088,23 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
       }
     }
 
-    // partial of (member, head h) for chunk c, in the decode kernel's layout: numerator
-    // element d at partial slot (d & 4 ? 64 : 0) + 4 (d >> 3) + (d & 3); O^T element rr of
-    // d-block md is d = 32 md + 8 (rr >> 2) + 4 half + (rr & 3), i.e. four consecutive slots
+    // partial of (member, head h) for chunk c, in the decode kernel's layout: the normalised
+    // output o / l in bf16 and (max, sum); O^T element rr of d-block md is
+    // d = 32 md + 8 (rr >> 2) + 4 half + (rr & 3), i.e. four consecutive elements
     const float l_tot = swap_halves_sum(l_i[0]);
     if (active && mem < nmem) {
       const int64_t unit = ((int64_t)seq * a.prefix_stride + c) * a.num_heads + h;
-      float* po = a.part_o + unit * D + 64 * half;
+      uint16_t* po = a.part_o + unit * D + 4 * half;
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
 #pragma unroll
       for (int md = 0; md < 4; ++md)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<float4*>(po + 16 * md + 4 * q) =
-              make_float4(o[0][md][4 * q], o[0][md][4 * q + 1], o[0][md][4 * q + 2], o[0][md][4 * q + 3]);
+        for (int q = 0; q < 4; ++q) {
+          uint2 w;
+          w.x = pack_bf16x2(o[0][md][4 * q] * inv, o[0][md][4 * q + 1] * inv);
+          w.y = pack_bf16x2(o[0][md][4 * q + 2] * inv, o[0][md][4 * q + 3] * inv);
+          *reinterpret_cast<uint2*>(po + 32 * md + 8 * q) = w;
+        }
       if (half == 0) *reinterpret_cast<float2*>(a.part_ml + unit * 2) = make_float2(m_i[0], l_tot);
     }
   }

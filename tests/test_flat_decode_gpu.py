@@ -69,8 +69,11 @@ def test_flat_serving_batch_matches_oracle(gpu):
 @pytest.mark.parametrize("n,lo,hi", [(128, 100, 2048), (16, 1024, 8192), (64, 1, 600)])
 def test_flat_and_split_grids_agree(gpu, n, lo, hi):
     """The same sequences through the flat grid (n <= 192) and the split grid (padded to
-    200 > 192 rows): both within tolerance of the oracle and within 4e-3 of each other; the
-    padding rows take no part (their cu_seqlens differences are 0 or negative)."""
+    200 > 192 rows): both within tolerance of the oracle and within the merge rounding of
+    each other (each path rounds its pieces' outputs to bf16 before the merge, an error
+    relative to the pieces' outputs rather than to the merged row, and rounds the merged row
+    once more); the padding rows take no part (their cu_seqlens differences are 0 or
+    negative)."""
     lens = W._uniform(torch.Generator().manual_seed(n + lo), lo, hi, n)
     w = _decode_batch(lens, n + lo, gpu)
     ids = list(range(0, n, max(1, n // 24)))
@@ -82,7 +85,13 @@ def test_flat_and_split_grids_agree(gpu, n, lo, hi):
     torch.cuda.synchronize()
     assert_close_bf16(flat[rows], want, "flat grid")
     assert_close_bf16(split[rows], want, "split grid")
-    assert (flat.float() - split.float()).abs().max().item() <= 4e-3
+    _assert_within_merge_rounding(flat, split)
+
+
+def _assert_within_merge_rounding(a, b):
+    a, b = a.float(), b.float()
+    bound = 2.0 ** -7 * torch.maximum(a.abs(), b.abs()) + 4e-3
+    assert ((a - b).abs() <= bound).all(), f"max diff {(a - b).abs().max().item():.3e}"
 
 
 def test_flat_long_sequences_merge_many_pieces(gpu):
@@ -100,7 +109,7 @@ def test_flat_long_sequences_merge_many_pieces(gpu):
 def test_flat_graph_padding_and_truncation(gpu):
     """Graph-padded tail rows (zero cu_seqlens) inside the flat grid's range, and a
     max_seqlen_k larger than every sequence (a captured graph's bound): the padding takes no
-    part and the results agree with the unpadded call to within the merge order (the two
+    part and the results agree with the unpadded call to within the merge rounding (the two
     launch bounds give slightly different run lengths)."""
     lens = W._uniform(torch.Generator().manual_seed(84), 300, 3000, 100)
     w = _decode_batch(lens, 84, gpu)
@@ -110,7 +119,7 @@ def test_flat_graph_padding_and_truncation(gpu):
     pad = pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, cu_q, cu_k, 1, w.max_seqlen_k + 1000, SCALE, True,
                                    bt, cached_prefix_keys=0)
     torch.cuda.synchronize()
-    assert (base.float() - pad.float()).abs().max().item() <= 4e-3
+    _assert_within_merge_rounding(base, pad)
 
 
 @pytest.mark.parametrize("hq,hkv", [(16, 8), (16, 2)])

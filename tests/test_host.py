@@ -80,7 +80,8 @@ def test_workspace_size_formula():
     ws = lib.pk_varlen_attention_workspace_bytes(256, HQ, HEAD_DIM, 1, 8192)
     split = 512
     units = 256 * (8192 // split) * HQ
-    want = math.ceil(units * HEAD_DIM * 4 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
+    want = math.ceil(units * HEAD_DIM * 2 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
+    # (bf16 outputs and fp32 (max, sum) per partial unit and head)
     # + the shared-prefix plan: item counts per chunk (1 KiB), then per (sequence, slot) one
     # item (32 B) and one member (8 B)
     want += math.ceil((1024 + 256 * (8192 // split) * 40) / 256) * 256
@@ -91,7 +92,7 @@ def test_workspace_size_formula():
     # key-line positions (130 ints in 256-byte lines)
     ws = lib.pk_varlen_attention_workspace_bytes(128, HQ, HEAD_DIM, 1, 2048)
     units = (128 * (2048 // 128) + 128 + 896) * HQ
-    want = math.ceil(units * HEAD_DIM * 4 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
+    want = math.ceil(units * HEAD_DIM * 2 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
     want += math.ceil(130 * 4 / 256) * 256
     want += math.ceil((1024 + 128 * (2048 // 128) * 40) / 256) * 256
     assert ws == want
