@@ -293,7 +293,7 @@ __device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char*
   // K A operand of half-tile mb, k-block kb, read in batches of kKBatch k-blocks (both
   // half-tiles) ahead of their MFMAs.
 #ifndef PK_PREFILL_KBATCH
-#define PK_PREFILL_KBATCH (kRowBlocks == 1 ? kHeadDim / 16 : kHeadDim / 32)
+#define PK_PREFILL_KBATCH 2  // k-blocks per batch of K reads (2, 4 and 8 measured alike)
 #endif
   constexpr int kKBatch = PK_PREFILL_KBATCH;
 #pragma unroll
@@ -558,9 +558,9 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
     l_i[rb] = 0.f;
   }
 
-  // Pipeline, one barrier per tile: at step n, the loads of tile n + 2 go out, tile n is
-  // computed from stage n & 1, tile n + 1 (registers) is written to stage (n + 1) & 1 -- last
-  // read at step n - 1, before the previous barrier -- and the barrier publishes it.
+  // Pipeline, one barrier per tile: at step n, tile n + 1 (registers) is written to stage
+  // (n + 1) & 1 and the loads of tile n + 2 go out into the same registers, tile n is computed
+  // from stage n & 1, and the barrier publishes tile n + 1.
   const int ntiles = te - tb;
   const int tbase = tb * TN;
   const LoadLanes ll = load_lanes(a, wave, lane, kTileKeys);
@@ -579,8 +579,14 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
       if (n >= ntiles) break;
       if (n == ntiles - 1) last_step();
       const int t0 = tbase + n * TN;
-      KvRegs Rn;
-      if (n + 2 < ntiles) load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, t0 + 2 * TN, ll, Rn);
+      // tile n + 1 (loaded during tile n - 1) goes to the other stage -- last read at step
+      // n - 1, before the previous barrier -- and its registers take tile n + 2's loads: one
+      // set of staging registers (a second set, holding tile n + 2 while tile n + 1 waited to
+      // be stored after tile n, took the kernel to 256 VGPRs with spills; 2.4% slower)
+      if (n + 1 < ntiles) {
+        store_tile_lds(R, KS[s ^ 1], VS[s ^ 1], wave, lane);
+        if (n + 2 < ntiles) load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, t0 + 2 * TN, ll, R);
+      }
       bool any = false, full[kRowBlocks];
 #pragma unroll
       for (int rb = 0; rb < kRowBlocks; ++rb) {
@@ -588,9 +594,7 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
         full[rb] = t0 + TN - 1 <= lim_lo[rb];
       }
       if (any) compute_tile(KS[s], VS[s], tl, qb, o, m_i, l_i, t0, lim, full, a.scale_log2, lane);
-      if (n + 1 < ntiles) store_tile_lds(R, KS[s ^ 1], VS[s ^ 1], wave, lane);
       lds_barrier();
-      R = Rn;
     }
   }
 
