@@ -47,8 +47,6 @@ struct AttnArgs {
   int32_t split_tokens;
   int32_t max_splits;           // partial slots per sequence (stride of part_o / part_ml)
   int32_t grid_splits;          // splits the decode grid covers per sequence
-  int32_t decode_ks;            // key sub-ranges (wavefronts) per split, set by the decode launch
-  int32_t decode_wq;            // kv-head quads (wavefronts) per sub-range, set by the decode launch
   // Flat decode grid (flat_groups > 0): the decode keys of the batch -- per decode sequence
   // b its keys after the shared prefix, c_b = Lk - min(prefix_keys, Lk) of them -- laid end
   // to end in sequence order (the key line: sequence b from position pos_b = c_0 + ... +

@@ -68,15 +68,6 @@ namespace {
 #endif
 
 constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
-// Small split grids give each split several wavefronts over sub-ranges of its keys (decode_unit):
-// up to PK_DECODE_SUB_RANGES of them while the grid stays under PK_DECODE_SUB_WAVES wavefronts.
-#ifndef PK_DECODE_SUB_RANGES
-#define PK_DECODE_SUB_RANGES 2   // 8 sequences of 256-2048 keys: 1 / 2 / 4 sub-ranges 18.6 / 18.0 / 19.4 us
-#endif
-#ifndef PK_DECODE_SUB_WAVES
-#define PK_DECODE_SUB_WAVES 4096
-#endif
-constexpr int kDecodeMaxSplitWaves = 8;  // wavefronts of a split work-group (quads x sub-ranges)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -344,32 +335,15 @@ __device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>
   }
 }
 
-// Softmax state floats per lane that a sub-range wavefront hands over in LDS: (m, l) and the
-// 8 numerator elements of each of the G heads.
-template <int G>
-constexpr int kSubStateFloats = G * 10;
-
 // One work unit: keys [t_begin, t_end) of decode sequence b (query row q0, keys from k0 in
 // flat mode, Lk keys in all) for the kv heads of this wavefront. direct: the unit holds every
 // key of the sequence, so it normalises and writes the output row itself; otherwise it
 // leaves its (max, sum, numerator) partial at partial unit unit0 (x num_heads) for the combine.
-// With a.decode_ks > 1 (small split grids) the unit's keys are cut into decode_ks sub-ranges
-// of whole pipeline steps, one per wavefront (sub = 0 .. decode_ks - 1, same kv heads): each
-// streams its own keys, the others hand their softmax state to sub-range 0 through LDS
-// (sub_lds: [decode_ks - 1][decode_wq][kSubStateFloats][64] floats) and it merges them and
-// stores, so a unit keeps one partial while more loads are in flight.
 template <int G, int U, bool PAGED, bool FUSED>
 __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_first, int b, int q0, int k0, int Lk,
-                                            int t_begin, int t_end, bool direct, int64_t unit0, int sub = 0,
-                                            int qw = 0, float* sub_lds = nullptr) {
+                                            int t_begin, int t_end, bool direct, int64_t unit0) {
   static_assert(U % 2 == 0, "P.V pairs keys");
   constexpr int D = kHeadDim;
-  const int ks = a.decode_ks;
-  if (ks > 1) {  // this wavefront's whole steps of the unit
-    const int per = ((t_end - t_begin + U - 1) / U + ks - 1) / ks * U;
-    t_begin = min(t_end, t_begin + sub * per);
-    t_end = min(t_end, t_begin + per);
-  }
   const int c = lane & 15;
   const int g_lane = g_first + (lane >> 4);               // this DPP row's kv head
   const bool row_live = g_lane < a.num_kv_heads;
@@ -412,9 +386,7 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
   // those are the reads worth keeping in L2 / Infinity Cache; everything past them is read
   // once per step and only displaces useful lines. Decided per split (by its first key).
   const bool stream = a.stream_from >= 0 && t_begin >= a.stream_from;
-  if (t_begin >= t_end) {
-    // an empty sub-range (its unit has fewer steps than sub-ranges): state stays (-inf, 0, 0)
-  } else if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
+  if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
     fused_producer<G>(a, st, q0, g, c, row_live, true);
     if (stream)
       decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, nothing);
@@ -424,36 +396,6 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
     decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
   } else {
     decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
-  }
-
-  if (ks > 1) {  // merge the sub-ranges' states into sub-range 0 (every wavefront reaches the barrier)
-    constexpr int F = kSubStateFloats<G>;
-    if (sub > 0) {
-      float* dst = sub_lds + ((size_t)((sub - 1) * a.decode_wq + qw) * F) * kWave + lane;
-#pragma unroll
-      for (int i = 0; i < G; ++i) {
-        dst[(10 * i) * kWave] = st.m[i];
-        dst[(10 * i + 1) * kWave] = st.l[i];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dst[(10 * i + 2 + e) * kWave] = st.acc[i][e];
-      }
-    }
-    __syncthreads();
-    if (sub > 0) return;
-    for (int r = 1; r < ks; ++r) {
-      const float* src = sub_lds + ((size_t)((r - 1) * a.decode_wq + qw) * F) * kWave + lane;
-#pragma unroll
-      for (int i = 0; i < G; ++i) {
-        const float mr = src[(10 * i) * kWave], lr = src[(10 * i + 1) * kWave];
-        const float mx = fmaxf(st.m[i], mr);
-        const float f0 = st.m[i] == -INFINITY ? 0.f : exp2_fast((st.m[i] - mx) * c2);
-        const float f1 = mr == -INFINITY ? 0.f : exp2_fast((mr - mx) * c2);
-        st.m[i] = mx;
-        st.l[i] = st.l[i] * f0 + lr * f1;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st.acc[i][e] = st.acc[i][e] * f0 + src[(10 * i + 2 + e) * kWave] * f1;
-      }
-    }
   }
 
   if (!row_live) return;
@@ -487,14 +429,11 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
 // Split mode: grid (splits x sequences, kv-head groups); a work-group takes split `split` of
 // one sequence (split_tokens keys after the shared prefix, if any).
 template <int G, int U, bool PAGED, bool FUSED>
-__global__ __launch_bounds__(kWave* kDecodeMaxSplitWaves) void decode_split_kernel(const AttnArgs a) {
-  extern __shared__ float sub_lds[];  // sub-range states (decode_ks > 1)
+__global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
-  // wavefront = (sub-range, kv-head quad of the group); the launch divides the kv heads
-  // evenly over the quads: every wavefront has >= 1 live row
-  const int qw = wave % a.decode_wq, sub = wave / a.decode_wq;
-  const int g_first = (blockIdx.y * a.decode_wq + qw) * 4;  // first kv head of the wave
+  // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
+  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
   // Work-groups are dispatched round-robin over the 8 XCDs in linear id order. Split-major
   // order with the sequence rotated by the split index sends consecutive splits of one
   // sequence to consecutive XCDs, so every XCD gets about 1/8 of each sequence whatever the
@@ -517,7 +456,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxSplitWaves) void decode_split_kern
   const int nsplit = (Pb + a.prefix_chunk - 1) / a.prefix_chunk + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
   const int slot = a.prefix_slots + split;
   decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, nsplit == 1,
-                                  ((int64_t)b * a.max_splits + slot) * a.num_heads, sub, qw, sub_lds);
+                                  ((int64_t)b * a.max_splits + slot) * a.num_heads);
 }
 
 // Inclusive sum over the wavefront: lane i gets x_0 + ... + x_i. DPP row shifts scan each
@@ -764,8 +703,6 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const dim3 block((unsigned)(waves * kWave));
   const bool fused = a.qkv != nullptr || a.new_k != nullptr;  // paged only (checked by their entry points)
   if (flat) {
-    a.decode_ks = 1;  // one wavefront per kv-head quad and piece
-    a.decode_wq = waves;
     const dim3 grid((unsigned)(a.flat_groups + a.num_seqs + 1), (unsigned)zgroups);  // + the recorder
     if (fused)
       hipLaunchKernelGGL((decode_flat_kernel<G, U, true, true>), grid, block, 0, stream, a);
@@ -776,23 +713,13 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
     return hipGetLastError();
   }
   if (a.grid_splits <= 0) return hipSuccess;  // every decode key lies in the shared prefix
-  const int64_t groups = (int64_t)a.grid_splits * a.num_seqs * zgroups;
-  // sub-ranges: while the grid is small and each sub-range keeps >= 2 pipeline steps
-  int ks = 1;
-  while (ks < PK_DECODE_SUB_RANGES && waves * 2 * ks <= kDecodeMaxSplitWaves &&
-         groups * waves * 2 * ks <= PK_DECODE_SUB_WAVES && a.split_tokens >= 2 * ks * 2 * U)
-    ks *= 2;
-  a.decode_ks = ks;
-  a.decode_wq = waves;
   const dim3 grid((unsigned)(a.grid_splits * a.num_seqs), (unsigned)zgroups);
-  const dim3 sblock((unsigned)(waves * ks * kWave));
-  const size_t lds = ks > 1 ? (size_t)(ks - 1) * waves * kSubStateFloats<G> * kWave * sizeof(float) : 0;
   if (fused)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, sblock, lds, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);
   else if (paged)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, sblock, lds, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, sblock, lds, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
