@@ -23,6 +23,7 @@
 //   * P.V: p rounded to bf16 and paired across two keys, one dot2 per (head, element).
 // Loads are software-pipelined two steps deep and all issued before the step's math.
 #include <algorithm>
+#include <type_traits>
 
 #include "norm_rope.h"
 
@@ -649,20 +650,33 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const A
     const int lane = threadIdx.x & (kWave - 1);
     float2 ml = make_float2(-INFINITY, 0.f);
     if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(lane) * H + h) * 2);
-    float v[kCombineFast];
+    // N unconditional loads (the next power of two >= nsplit, at least 8), issued with the
+    // (max, sum) loads: past nsplit the last partial is read again, and its weight there is 0.
+    // (A conditional 16-bit load per split compiles to a branch and a wait per split; all 64
+    // loads for every sequence cost cfg2's combine 6 -> 9.4 us.)
+    const auto merge = [&](auto n_tag) {
+      constexpr int N = decltype(n_tag)::value;
+      float v[N];
 #pragma unroll
-    // branch-free: past nsplit the last partial is read again, and its weight there is 0
-    // (a conditional 16-bit load per split compiles to a branch and a wait per split)
-    for (int j = 0; j < kCombineFast; ++j) v[j] = bf16_to_f32(po[unit_of(min(j, nsplit - 1)) * stride]);
-    const float rm = row16_max(ml.x);
-    const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
-    const float w = lane < nsplit ? exp2_fast(ml.x - mx) * ml.y : 0.f;  // each partial's weight: its share of l
-    const float rs = row16_sum(w);
-    const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
-    float acc = 0.f;
+      for (int j = 0; j < N; ++j) v[j] = bf16_to_f32(po[unit_of(min(j, nsplit - 1)) * stride]);
+      const float rm = row16_max(ml.x);
+      const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
+      const float w = lane < nsplit ? exp2_fast(ml.x - mx) * ml.y : 0.f;  // each partial's weight: its share of l
+      const float rs = row16_sum(w);
+      const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
+      float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < kCombineFast; ++j) acc = fmaf(lane_value(w, j), v[j], acc);
-    a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(acc / lsum);
+      for (int j = 0; j < N; ++j) acc = fmaf(lane_value(w, j), v[j], acc);
+      a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(acc / lsum);
+    };
+    if (nsplit <= 8)
+      merge(std::integral_constant<int, 8>{});
+    else if (nsplit <= 16)
+      merge(std::integral_constant<int, 16>{});
+    else if (nsplit <= 32)
+      merge(std::integral_constant<int, 32>{});
+    else
+      merge(std::integral_constant<int, kCombineFast>{});
     return;
   }
   // Long contexts: split maxima and weights by block reductions into LDS, then thread d
