@@ -17,6 +17,10 @@ constexpr int kHeadDim = 128;   // the only head_dim built (Qwen3 family)
 constexpr int kWave = 64;       // CDNA wavefront width
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
 // Everything the attention kernels need; passed by value as the kernel argument.
@@ -59,6 +63,15 @@ struct AttnArgs {
   int32_t flat_step;
   int32_t flat_unit0;
   int32_t* flat_meta;
+  // Mixed path (mixed_decode != 0, calls with prefill rows): the prefill plan lays out the
+  // decode rows on the flat grid's key line (flat_groups runs) and lists the pieces that
+  // exist in dec_pieces ([piece][2] int4: (sequence, q0, k0, Lk), (t_begin, t_end, direct,
+  // partial unit)); the persistent prefill kernel runs them, one (piece, kv-head quad) per
+  // wavefront claim, and the merge kernel performs their combines. Work-groups of the first
+  // mixed_prefill_xcds XCDs start on prefill items, the others on decode pieces.
+  int32_t mixed_decode;
+  int32_t mixed_prefill_xcds;
+  int4* dec_pieces;
   // Shared-prefix decode: keys [0, min(prefix_keys, Lk)) of a decode sequence are computed by
   // the shared-prefix kernel, one partial per chunk of prefix_chunk keys in slots
   // [0, prefix_slots); the decode kernel covers the keys after them (split grid: its split s
@@ -128,6 +141,11 @@ constexpr int kPrefillSlotsMax = 256;
 constexpr int kPrefillQueueStride = 32;  // claim counter q at pf_queue[32 q]: one 128-byte line each
 constexpr int kPrefillQueueMeta = 8 * kPrefillQueueStride;  // then item count, merge count, split size
 constexpr int kPrefillQueueInts = kPrefillQueueMeta + 64;   // header ints (1280 bytes)
+// Mixed path: decode work units (pieces x kv-head quads) in the header's meta line, their
+// claim counter on a 128-byte line of its own.
+constexpr int kDecodeUnitsMeta = kPrefillQueueMeta + 3;
+constexpr int kDecodeClaim = kPrefillQueueMeta + 32;
+constexpr int kMixedMaxSeqs = 1023;  // the plan kernel's threads hold one sequence each
 constexpr int kPrefillRows = 256;       // query rows per work item (query tokens x GQA heads)
 constexpr int kPrefillPartCap = 3 * kPrefillSlotsMax;
 constexpr int kPrefillMergeCap = 3 * kPrefillSlotsMax / 2;
@@ -138,6 +156,7 @@ inline int64_t prefill_item_cap(int num_seqs, int num_heads, int max_seqlen_q) {
          kPrefillPartCap;
 }
 
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

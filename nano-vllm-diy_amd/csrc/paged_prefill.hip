@@ -86,7 +86,6 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Value of lane l ^ 32 (the other half of the wavefront), one VALU swap.
 __device__ __forceinline__ float swap_halves_max(float v) {
@@ -134,8 +133,6 @@ __device__ __forceinline__ int v_chunk(int r, int s) {
 constexpr int kRowsPerWave = kTileKeys / kPrefillWaves;
 constexpr int kLoadsPerOperand = kRowsPerWave / 4;
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Per-lane source offsets (elements) of the rows this lane moves.
 struct LoadLanes {
