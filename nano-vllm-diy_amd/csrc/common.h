@@ -63,15 +63,6 @@ struct AttnArgs {
   int32_t flat_step;
   int32_t flat_unit0;
   int32_t* flat_meta;
-  // Mixed path (mixed_decode != 0, calls with prefill rows): the prefill plan lays out the
-  // decode rows on the flat grid's key line (flat_groups runs) and lists the pieces that
-  // exist in dec_pieces ([piece][2] int4: (sequence, q0, k0, Lk), (t_begin, t_end, direct,
-  // partial unit)); the persistent prefill kernel runs them, one (piece, kv-head quad) per
-  // wavefront claim, and the merge kernel performs their combines. Work-groups of the first
-  // mixed_prefill_xcds XCDs start on prefill items, the others on decode pieces.
-  int32_t mixed_decode;
-  int32_t mixed_prefill_xcds;
-  int4* dec_pieces;
   // Shared-prefix decode: keys [0, min(prefix_keys, Lk)) of a decode sequence are computed by
   // the shared-prefix kernel, one partial per chunk of prefix_chunk keys in slots
   // [0, prefix_slots); the decode kernel covers the keys after them (split grid: its split s
@@ -141,11 +132,6 @@ constexpr int kPrefillSlotsMax = 256;
 constexpr int kPrefillQueueStride = 32;  // claim counter q at pf_queue[32 q]: one 128-byte line each
 constexpr int kPrefillQueueMeta = 8 * kPrefillQueueStride;  // then item count, merge count, split size
 constexpr int kPrefillQueueInts = kPrefillQueueMeta + 64;   // header ints (1280 bytes)
-// Mixed path: decode work units (pieces x kv-head quads) in the header's meta line, their
-// claim counter on a 128-byte line of its own.
-constexpr int kDecodeUnitsMeta = kPrefillQueueMeta + 3;
-constexpr int kDecodeClaim = kPrefillQueueMeta + 32;
-constexpr int kMixedMaxSeqs = 1023;  // the plan kernel's threads hold one sequence each
 constexpr int kPrefillRows = 256;       // query rows per work item (query tokens x GQA heads)
 constexpr int kPrefillPartCap = 3 * kPrefillSlotsMax;
 constexpr int kPrefillMergeCap = 3 * kPrefillSlotsMax / 2;

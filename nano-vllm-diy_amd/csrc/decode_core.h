@@ -1,8 +1,6 @@
-// Device code of the paged decode path shared by the decode kernels (paged_decode.hip) and
-// the persistent chunked-prefill kernel, which runs a mixed batch's decode rows beside its
-// prefill items (paged_prefill.hip): the register-direct K/V pipeline, the fused producer and
-// one decode work unit. (Included inside each file's own translation unit: no device code is
-// linked across files.)
+// Device code of the paged decode path, kept apart from the kernels that run it
+// (paged_decode.hip): the register-direct K/V pipeline, the fused producer, one decode work
+// unit, and the per-(sequence, head) body of the combine pass.
 #pragma once
 
 #include "norm_rope.h"
