@@ -78,6 +78,10 @@ def test_engine_sizes_kv_cache_from_free_memory(gpu):
     from pagedkv.runner import kv_cache_num_blocks
 
     cfg = Qwen3Config(num_hidden_layers=2)
+    # the sizing subtracts the allocator's peak above its current allocation (a forward pass's
+    # activations): start from this test's own peak, not from earlier tests' larger batches
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats(gpu)
     free, total = torch.cuda.mem_get_info(gpu)
     util = (total - free) / total + 0.02                  # about 2% of the device for the cache
     eng = E.LLMEngine(cfg, device=gpu, max_live_seqs=8, max_seq_len=1024, enforce_eager=True,
