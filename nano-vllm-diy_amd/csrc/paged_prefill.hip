@@ -768,49 +768,67 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel
 // w_s = exp2(m_s - max_s m_s) l_s, o_s the split's normalised output (bf16). Work item =
 // (split unit, quarter of head_dim, kv head); thread t owns row t of the unit and 8 chunks
 // of 4 dims. At most 4 wavefronts per SIMD: the register budget lets the loads of
-// kMergeLoads splits be in flight at once.
+// kMergeLoads splits be in flight at once. Two rounds of loads reach the first store: the
+// work-list entry (the first one read together with the work count, from a list slot that
+// always exists), then the sequence's bounds with the partials (which do not depend on
+// them; rows past the sequence are dropped at the store).
 template <int G>
 __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void prefill_merge_kernel(
     const AttnArgs a) {
   constexpr int D = kHeadDim;
   constexpr int TM = kPrefillRows / G;
   constexpr int CQ = 8;  // chunks per quarter
-  const int nw = (int)min((int64_t)a.pf_queue[kPrefillQueueMeta + 1], (int64_t)a.pf_merge_cap * a.num_kv_heads) * 4;
   const int r = threadIdx.x;
   const int hkv = a.num_kv_heads;
   // w = (unit, quarter) * hkv + g: with 8 kv heads, head g's merges run on XCD g (work-groups
   // go to XCDs round-robin and the grid is a multiple of 8), where the prefill kernel's
   // sub-queue g wrote its partials, so the reads mostly hit that XCD's L2
-  for (int w = blockIdx.x; w < nw; w += gridDim.x) {
+  const auto entry = [&](int w) { return a.pf_merges[min((w / hkv) >> 2, a.pf_merge_cap - 1)]; };
+  int w = blockIdx.x;
+  int4 e = entry(w);
+  const int merges = a.pf_queue[kPrefillQueueMeta + 1];
+  // the entry is consumed here, so its load goes out with the count's, not after the loop test
+  asm volatile("" ::"v"(e.x), "v"(e.y), "v"(e.z), "v"(e.w));
+  const int nw = (int)min((int64_t)merges, (int64_t)a.pf_merge_cap * hkv) * 4;
+  for (; w < nw; w += gridDim.x, e = entry(w)) {
     const int rest = w / hkv;
     const int g = w - rest * hkv;
     const int c0 = (rest & 3) * CQ;
-    const int unit = rest >> 2;
-    const int4 e = a.pf_merges[unit];
-    const int b = e.x;
-    const int qt = e.y;
-    const int pg = e.z;
-    const int n = e.w;
+    const int b = __builtin_amdgcn_readfirstlane(e.x);  // one entry per work-group
+    const int qt = __builtin_amdgcn_readfirstlane(e.y);
+    const int pg = __builtin_amdgcn_readfirstlane(e.z);
+    const int n = __builtin_amdgcn_readfirstlane(e.w);
     if (b < 0 || b >= a.num_seqs || pg < 0 || n <= 0) continue;  // see prefill_item
+    if ((int64_t)(pg + n) * hkv > a.pf_part_cap) continue;       // the plan bounds partial ids
     const int q0 = a.cu_q[b];
-    const int Lq = a.cu_q[b + 1] - q0;
+    const int q1 = a.cu_q[b + 1];
     const int tok = qt * TM + r % TM;
     const int h = g * G + r / TM;
-    if (tok >= Lq) continue;
-    if ((int64_t)(pg + n) * hkv > a.pf_part_cap) continue;  // the plan bounds partial ids
     // Every load below reads a valid split (index clamped to the last one) and a split past
-    // the end gets weight 0: no load sits behind a branch, so the compiler's wait counts see
-    // a whole batch in flight instead of waiting out each load in turn.
+    // the end gets weight 0 by arithmetic on the loaded values (max - inf, sum x 0), which
+    // keeps every load unconditional: no load sits behind a branch, so the compiler's wait
+    // counts see a whole batch in flight instead of waiting out each load in turn.
     const int last = n - 1;
     const float* ml_base = a.pf_part_ml + ((int64_t)(pg * hkv + g) * kPrefillRows + r) * 2;
     const int64_t ml_step = (int64_t)hkv * kPrefillRows * 2;  // next split of the unit
     const auto load_ml = [&](int s2) {
       const float2 v = *reinterpret_cast<const float2*>(ml_base + min(s2, last) * ml_step);
-      return s2 < n ? v : make_float2(-INFINITY, 0.f);
+      return make_float2(v.x + (s2 < n ? 0.f : -INFINITY), v.y * (s2 < n ? 1.f : 0.f));
+    };
+    const int64_t po_step = (int64_t)hkv * (32 * kPrefillRows * 4);
+    const uint16_t* po_base = a.pf_part_o + (int64_t)(pg * hkv + g) * (32 * kPrefillRows * 4) +
+                              ((int64_t)c0 * kPrefillRows + r) * 4;
+    const auto load = [&](int s2, uint2 (&v)[CQ]) {
+#pragma unroll
+      for (int c = 0; c < CQ; ++c)
+        v[c] = *reinterpret_cast<const uint2*>(po_base + min(s2, last) * po_step + (int64_t)c * kPrefillRows * 4);
     };
     float2 ml[kMergeBatch];
 #pragma unroll
     for (int s2 = 0; s2 < kMergeBatch; ++s2) ml[s2] = load_ml(s2);
+    uint2 v[kMergeLoads][CQ];
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) load(j, v[j]);
     float M = -INFINITY;
 #pragma unroll
     for (int s2 = 0; s2 < kMergeBatch; ++s2) M = fmaxf(M, ml[s2].x);
@@ -819,38 +837,28 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
     for (int c = 0; c < CQ; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.f;
-    if (M != -INFINITY) {
-      const int64_t po_step = (int64_t)hkv * (32 * kPrefillRows * 4);
-      const uint16_t* po_base = a.pf_part_o + (int64_t)(pg * hkv + g) * (32 * kPrefillRows * 4) +
-                                ((int64_t)c0 * kPrefillRows + r) * 4;
-      const auto load = [&](int s2, uint2 (&v)[CQ]) {
+    // weight 0 for a split past the end or that saw no key (and for every split of a row that
+    // saw none: M = -inf)
+    const auto add = [&](float2 m, const uint2 (&vv)[CQ]) {
+      const float wgt = M == -INFINITY ? 0.f : exp2_fast(m.x - M) * m.y;
+      L += wgt;
 #pragma unroll
-        for (int c = 0; c < CQ; ++c)
-          v[c] = *reinterpret_cast<const uint2*>(po_base + min(s2, last) * po_step + (int64_t)c * kPrefillRows * 4);
-      };
-      const auto add = [&](float2 m, const uint2 (&v)[CQ]) {
-        const float wgt = exp2_fast(m.x - M) * m.y;  // 0 for a split past the end or that saw no key
-        L += wgt;
-#pragma unroll
-        for (int c = 0; c < CQ; ++c) {
-          acc[c].x += wgt * bf16_lo(v[c].x);
-          acc[c].y += wgt * bf16_hi(v[c].x);
-          acc[c].z += wgt * bf16_lo(v[c].y);
-          acc[c].w += wgt * bf16_hi(v[c].y);
-        }
-      };
-      uint2 v[kMergeLoads][CQ];
-#pragma unroll
-      for (int j = 0; j < kMergeLoads; ++j) load(j, v[j]);
-#pragma unroll
-      for (int j = 0; j < kMergeLoads; ++j) add(ml[j], v[j]);
-      for (int s0 = kMergeLoads; s0 < n; s0 += kMergeLoads) {  // units of many splits
-#pragma unroll
-        for (int j = 0; j < kMergeLoads; ++j) load(s0 + j, v[j]);
-#pragma unroll
-        for (int j = 0; j < kMergeLoads; ++j) add(load_ml(s0 + j), v[j]);
+      for (int c = 0; c < CQ; ++c) {
+        acc[c].x += wgt * bf16_lo(vv[c].x);
+        acc[c].y += wgt * bf16_hi(vv[c].x);
+        acc[c].z += wgt * bf16_lo(vv[c].y);
+        acc[c].w += wgt * bf16_hi(vv[c].y);
       }
+    };
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) add(ml[j], v[j]);
+    for (int s0 = kMergeLoads; s0 < n; s0 += kMergeLoads) {  // units of many splits
+#pragma unroll
+      for (int j = 0; j < kMergeLoads; ++j) load(s0 + j, v[j]);
+#pragma unroll
+      for (int j = 0; j < kMergeLoads; ++j) add(load_ml(s0 + j), v[j]);
     }
+    if (tok >= q1 - q0) continue;  // row past the sequence
     const float inv = L > 0.f ? 1.f / L : 0.f;
     uint16_t* op = a.out + (int64_t)(q0 + tok) * a.out_row_stride + h * D + 4 * c0;
 #pragma unroll
