@@ -415,6 +415,9 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
     int rc = hip_status(pk::launch_shared_prefix(a, group, s), "shared-prefix launch");
     if (rc != PK_OK) return rc;
   }
+  // with prefill rows the decode partials are merged by the prefill merge kernel, which the
+  // call launches anyway (one launch fewer)
+  a.combine_in_merge = max_seqlen_q > 1;
   int rc = hip_status(pk::launch_decode(a, group, paged, max_seqlen_k, s), "decode launch");
   if (rc != PK_OK) return rc;
   if (max_seqlen_q > 1)

@@ -48,6 +48,7 @@ struct AttnArgs {
   float* part_ml;               // [unit][num_heads][2] = (max in the exp2 domain, sum)
   int32_t stream_from;           // decode splits starting at key >= this use non-temporal loads (< 0: none)
   int32_t store_through;         // decode partials written through L2 (set by the decode launch)
+  int32_t combine_in_merge;      // the decode combines run in the prefill merge kernel
   int32_t split_tokens;
   int32_t max_splits;           // partial slots per sequence (stride of part_o / part_ml)
   int32_t grid_splits;          // splits the decode grid covers per sequence

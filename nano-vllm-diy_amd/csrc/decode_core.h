@@ -8,6 +8,12 @@
 namespace pk {
 namespace {
 
+#ifndef PK_DECODE_STEP_G2
+#define PK_DECODE_STEP_G2 8     // keys per pipeline step for GQA groups <= 2
+#endif
+// Keys per pipeline step of the decode units built for a GQA group.
+constexpr int decode_step_keys(int group) { return group <= 2 ? PK_DECODE_STEP_G2 : 4; }
+
 constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through L2
 // Partial footprint (launch bound: sequences x splits x heads x D x 4 bytes) above which the
 // partials are written through L2. The eight XCD L2s hold 32 MB together: smaller partial
@@ -373,44 +379,27 @@ __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
   return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
-// Merge the per-split partials of one (sequence, head). A separate launch (rather than a
-// "last work-group merges" tail in the split kernel) because the XCD L2 caches are not
-// coherent with each other: a device-scope fence per work-group would write back and
-// invalidate a whole L2, while the kernel boundary makes every partial visible for free.
-// Up to kCombineFast splits are merged from registers in two dependent memory round trips
-// (the sequence's lengths, then all partials at once); longer contexts take the LDS path.
+// Merge the per-split partials of one (sequence, head). A separate pass (rather than a "last
+// work-group merges" tail in the split kernel) because the XCD L2 caches are not coherent
+// with each other: a device-scope fence per work-group would write back and invalidate a
+// whole L2, while a kernel boundary makes every partial visible for free. The merge runs
+// from registers in 128 consecutive threads (two whole wavefronts, thread d = output element
+// d) with no LDS and no barrier, so any kernel can run it on part of a work-group: the decode
+// combine launch, or the prefill merge kernel of a call with prefill rows.
 constexpr int kCombineThreads = kHeadDim;  // thread d owns output element d
-constexpr int kCombineMaxSplits = 256;     // splits per sequence the weight table holds
-
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
-  for (int m = kWave / 2; m >= 1; m >>= 1) {
-    const float o = xor_shfl(v, m);
-    v = is_max ? fmaxf(v, o) : v + o;
-  }
-  const int wave = threadIdx.x / kWave;
-  __syncthreads();  // red may still be read by a previous reduction
-  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
-  __syncthreads();
-  v = red[0];
-  for (int w = 1; w < kCombineThreads / kWave; ++w) v = is_max ? fmaxf(v, red[w]) : v + red[w];
-  return v;
-}
+constexpr int kCombineMaxSplits = 256;     // partials per sequence the launches are sized for
 
 #ifndef PK_COMBINE_FAST
 #define PK_COMBINE_FAST 64
 #endif
-// Splits merged from registers, without LDS: lane j of each wavefront holds split j's
-// (max, sum), so at most one wavefront's width. Measured on 8 sequences of 256-2048 keys
-// (29 splits of 64 keys): 4.9 us against 5.6 us on the LDS path (16-split register path).
+// Partials merged in one round of loads: lane j of each wavefront holds partial j's (max,
+// sum), so at most one wavefront's width; longer sequences take rounds of this many.
 constexpr int kCombineFast = PK_COMBINE_FAST;
 static_assert(kCombineFast <= kWave && (kCombineFast & (kCombineFast - 1)) == 0, "one lane per split");
 
-// The merge of one (sequence, head): thread d of 128 consecutive threads (two whole
-// wavefronts) owns output element d. FAST_ONLY (callers whose sequences have at most
-// kCombineFast partials) leaves out the LDS path, whose block reductions assume the 128
-// threads are the whole work-group; w_s and red are that path's LDS arrays.
-template <bool FAST_ONLY>
-__device__ __forceinline__ void combine_row(const AttnArgs& a, int b, int h, int d, float* w_s, float* red) {
+// The merge of one (sequence, head) by the 128 threads whose element is d (threadIdx.x & 63
+// is the lane inside each of their two wavefronts).
+__device__ __forceinline__ void combine_row(const AttnArgs& a, int b, int h, int d) {
   constexpr int D = kHeadDim;
   const int q0 = a.cu_q[b];
   const int q1 = a.cu_q[b + 1];
@@ -446,72 +435,54 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int b, int h, int
     post0 = (int64_t)b * a.max_splits + a.prefix_slots - npre;
   }
   if (nsplit <= 1 && npre == 0) return;  // written directly by the decode kernel
-  nsplit = min(nsplit, FAST_ONLY ? kCombineFast : kCombineMaxSplits);  // the launch keeps it within
+  nsplit = min(nsplit, kCombineMaxSplits);  // the launches keep it within
   const auto unit_of = [&](int j) -> int64_t { return j < npre ? pre0 + j : post0 + j; };
   const uint16_t* po = a.part_o + (int64_t)h * D + d;
   const int64_t stride = (int64_t)H * D;
-  if (FAST_ONLY || nsplit <= kCombineFast) {
-    // Every load of the merge is issued at once: lane j < nsplit of each wavefront reads
-    // split j's (max, sum), thread d element d of every split. The weights are formed in
-    // lanes 0 .. kCombineFast - 1 and broadcast by shuffles: no LDS, no barrier.
-    // Reductions are DPP row steps plus reads of the four rows' lanes, and weight j reaches
-    // every lane by a readlane: no LDS permutes on the dependency chain.
-    const int lane = threadIdx.x & (kWave - 1);
+  const int lane = threadIdx.x & (kWave - 1);
+  // (max, sum, weighted sum of element d) of partials j0 .. j0 + cnt - 1. Every load of the
+  // round is issued at once: lane j < cnt of each wavefront reads partial j0 + j's (max, sum),
+  // thread d element d of N partials (N >= cnt a power of two, at least 8; past cnt the last
+  // partial is read again and weighted 0: a conditional 16-bit load per partial compiles to a
+  // branch and a wait per partial, and 64 loads for every sequence cost cfg2's combine
+  // 6 -> 9.4 us). The weights are formed in lanes 0 .. kCombineFast - 1; reductions are DPP
+  // row steps plus reads of the four rows' lanes, and weight j reaches every lane by a
+  // readlane: no LDS permutes on the dependency chain.
+  const auto round = [&](int j0, int cnt, auto n_tag) {
+    constexpr int N = decltype(n_tag)::value;
     float2 ml = make_float2(-INFINITY, 0.f);
-    if (lane < nsplit) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(lane) * H + h) * 2);
-    // N unconditional loads (the next power of two >= nsplit, at least 8), issued with the
-    // (max, sum) loads: past nsplit the last partial is read again, and its weight there is 0.
-    // (A conditional 16-bit load per split compiles to a branch and a wait per split; all 64
-    // loads for every sequence cost cfg2's combine 6 -> 9.4 us.)
-    const auto merge = [&](auto n_tag) {
-      constexpr int N = decltype(n_tag)::value;
-      float v[N];
+    if (lane < cnt) ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(j0 + lane) * H + h) * 2);
+    float v[N];
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[j] = bf16_to_f32(po[unit_of(min(j, nsplit - 1)) * stride]);
-      const float rm = row16_max(ml.x);
-      const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
-      const float w = lane < nsplit ? exp2_fast(ml.x - mx) * ml.y : 0.f;  // each partial's weight: its share of l
-      const float rs = row16_sum(w);
-      const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
-      float acc = 0.f;
+    for (int j = 0; j < N; ++j) v[j] = bf16_to_f32(po[unit_of(j0 + min(j, cnt - 1)) * stride]);
+    const float rm = row16_max(ml.x);
+    const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
+    const float w = lane < cnt ? exp2_fast(ml.x - mx) * ml.y : 0.f;  // each partial's share of l
+    const float rs = row16_sum(w);
+    const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
+    float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < N; ++j) acc = fmaf(lane_value(w, j), v[j], acc);
-      a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(acc / lsum);
-    };
-    if (nsplit <= 8)
-      merge(std::integral_constant<int, 8>{});
-    else if (nsplit <= 16)
-      merge(std::integral_constant<int, 16>{});
-    else if (nsplit <= 32)
-      merge(std::integral_constant<int, 32>{});
-    else
-      merge(std::integral_constant<int, kCombineFast>{});
-    return;
+    for (int j = 0; j < N; ++j) acc = fmaf(lane_value(w, j), v[j], acc);
+    return make_float3(mx, lsum, acc);
+  };
+  float3 r;
+  if (nsplit <= 8)
+    r = round(0, nsplit, std::integral_constant<int, 8>{});
+  else if (nsplit <= 16)
+    r = round(0, nsplit, std::integral_constant<int, 16>{});
+  else if (nsplit <= 32)
+    r = round(0, nsplit, std::integral_constant<int, 32>{});
+  else
+    r = round(0, min(nsplit, kCombineFast), std::integral_constant<int, kCombineFast>{});
+  // Longer sequences: further rounds of kCombineFast partials folded into the running
+  // (max, sum, numerator), each rescaled to the larger max.
+  for (int j0 = kCombineFast; j0 < nsplit; j0 += kCombineFast) {
+    const float3 t = round(j0, min(nsplit - j0, kCombineFast), std::integral_constant<int, kCombineFast>{});
+    const float m = fmaxf(r.x, t.x);
+    const float sa = exp2_fast(r.x - m), sb = exp2_fast(t.x - m);
+    r = make_float3(m, r.y * sa + t.y * sb, r.z * sa + t.z * sb);
   }
-  // Long contexts: split maxima and weights by block reductions into LDS, then thread d
-  // forms the weighted sum of element d with four independent accumulators.
-  float mx = -INFINITY;
-  for (int j = threadIdx.x; j < nsplit; j += kCombineThreads)
-    mx = fmaxf(mx, a.part_ml[(unit_of(j) * H + h) * 2]);
-  mx = block_reduce(mx, true, red);
-  float lsum = 0.f;
-  for (int j = threadIdx.x; j < nsplit; j += kCombineThreads) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (unit_of(j) * H + h) * 2);
-    const float w = exp2_fast(ml.x - mx) * ml.y;
-    w_s[j] = w;
-    lsum += w;
-  }
-  lsum = block_reduce(lsum, false, red);  // its barriers also publish w_s
-  float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-  int j = 0;
-  for (; j + 4 <= nsplit; j += 4) {
-    o0 = fmaf(w_s[j], bf16_to_f32(po[unit_of(j) * stride]), o0);
-    o1 = fmaf(w_s[j + 1], bf16_to_f32(po[unit_of(j + 1) * stride]), o1);
-    o2 = fmaf(w_s[j + 2], bf16_to_f32(po[unit_of(j + 2) * stride]), o2);
-    o3 = fmaf(w_s[j + 3], bf16_to_f32(po[unit_of(j + 3) * stride]), o3);
-  }
-  for (; j < nsplit; ++j) o0 = fmaf(w_s[j], bf16_to_f32(po[unit_of(j) * stride]), o0);
-  a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(((o0 + o1) + (o2 + o3)) / lsum);
+  a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(r.z / r.y);
 }
 
 }  // namespace

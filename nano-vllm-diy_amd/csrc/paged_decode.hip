@@ -34,9 +34,6 @@ namespace {
 #ifndef PK_DECODE_WAVES
 #define PK_DECODE_WAVES 4       // max wavefronts (4 kv heads each) per work-group
 #endif
-#ifndef PK_DECODE_STEP_G2
-#define PK_DECODE_STEP_G2 8     // keys per pipeline step for GQA groups <= 2
-#endif
 #ifndef PK_DECODE_SPLIT_MAX
 #define PK_DECODE_SPLIT_MAX 512 // keys per work unit (split) when the batch is large
 #endif
@@ -195,9 +192,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(con
 }
 
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const AttnArgs a) {
-  __shared__ float w_s[kCombineMaxSplits];
-  __shared__ float red[kCombineThreads / kWave];
-  combine_row<false>(a, blockIdx.y, blockIdx.x, threadIdx.x, w_s, red);
+  combine_row(a, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
 template <int G, int U>
@@ -231,9 +226,6 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
     hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
-
-// Keys per pipeline step of the decode kernels built for a GQA group.
-constexpr int decode_step_keys(int group) { return group <= 2 ? PK_DECODE_STEP_G2 : 4; }
 
 }  // namespace
 
@@ -290,7 +282,8 @@ hipError_t launch_decode(const AttnArgs& args, int group, bool paged, int max_se
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;
-  if (a.max_splits > 1 || a.flat_groups > 0) {
+  // (a call with prefill rows merges the decode partials in its prefill merge kernel)
+  if ((a.max_splits > 1 || a.flat_groups > 0) && !a.combine_in_merge) {
     hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)a.num_heads, (unsigned)a.num_seqs),
                        dim3(kCombineThreads), 0, stream, a);
     err = hipGetLastError();

@@ -42,7 +42,7 @@
 // the k-order of the instruction is permuted (same permutation on the V side).
 #include <algorithm>
 
-#include "common.h"
+#include "decode_core.h"
 
 namespace pk {
 namespace {
@@ -869,6 +869,19 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
       *reinterpret_cast<uint2*>(op + 4 * c) = wv;
     }
   }
+  // The decode rows' combines (their partials were left by this call's decode launch, which
+  // runs first): one (sequence, head) per 128 threads, continuing the work-group order after
+  // the split-unit merges so the groups with fewer of those start on these.
+  if (a.combine_in_merge) {
+    const int pairs = a.num_seqs * a.num_heads;
+    const int half = (int)(threadIdx.x >> 7);
+    const int grid = (int)gridDim.x;
+    const int first = (int)((blockIdx.x + grid - nw % grid) % grid);
+    for (int pr = 2 * first + half; pr < pairs; pr += 2 * grid) {
+      const int b = pr / a.num_heads;
+      combine_row(a, b, pr - b * a.num_heads, threadIdx.x & (kCombineThreads - 1));
+    }
+  }
 }
 
 // ---- Shared-prefix decode ------------------------------------------------------------------
@@ -1146,6 +1159,7 @@ hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_
   AttnArgs pa = a;
   pa.prefill_qtiles = (max_seqlen_q + TM - 1) / TM;
   pa.pf_slots = device_prefill_slots();
+  pa.flat_step = decode_step_keys(G);  // the decode pieces' step, for the combines in the merge kernel
   if (paged)
     return causal ? launch_prefill_gpc<G, true, true>(pa, stream) : launch_prefill_gpc<G, true, false>(pa, stream);
   return causal ? launch_prefill_gpc<G, false, true>(pa, stream) : launch_prefill_gpc<G, false, false>(pa, stream);
