@@ -232,7 +232,7 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
 int decode_split_tokens(int num_seqs, int max_seqlen_k) {
   // PK_DECODE_SPLIT_MAX keys per work-group when the batch yields enough work-groups to
   // cover the 256 CUs several times, shorter splits for small batches; longer ones when
-  // the combine pass's weight table (kCombineMaxSplits per sequence) would overflow.
+  // sequences would have more than kCombineMaxSplits partials (what the combine is sized for).
   const auto splits = [&](int split) { return (int64_t)(max_seqlen_k + split - 1) / split; };
   int split = PK_DECODE_SPLIT_MAX;
   while (split > PK_DECODE_MIN_SPLIT && (int64_t)num_seqs * splits(split) < PK_DECODE_MIN_GROUPS &&

@@ -6,7 +6,7 @@ splits; a sequence's pieces are merged by the combine pass from partial units b 
 tests hold that grid to the oracle (attention.py:95-104 decode rows) on serving-sized
 batches, against the split grid on the same sequences (the split grid is selected by padding
 the batch past 192 sequences with zero-length rows, as graph padding does), on sequences
-long enough to need more pieces than the combine's register path merges, and on the two
+long enough to need more pieces than one round of the combine's loads merges, and on the two
 one-launch decode steps (store + decode, norm + RoPE + store + decode), which must stay
 bit-identical to their unfused sequences.
 """
@@ -95,8 +95,8 @@ def _assert_within_merge_rounding(a, b):
 
 
 def test_flat_long_sequences_merge_many_pieces(gpu):
-    """Two 40k-key sequences among short ones: their pieces (~250 each) exceed the combine's
-    64-lane register path, so they merge through its LDS path."""
+    """Two 40k-key sequences among short ones: their pieces (~250 each) exceed one round of
+    the combine's loads (64 partials), so they merge in several rounds folded together."""
     lens = [40000, 38111, 300, 5, 1, 2047]
     w = _decode_batch(lens, 83, gpu)
     rows, want = subset_oracle(w, list(range(len(lens))))
