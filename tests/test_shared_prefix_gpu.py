@@ -191,3 +191,32 @@ def test_prefix_below_one_chunk_is_the_plain_path(gpu):
     plain = _run(b, None, hint=BS - 56)
     torch.cuda.synchronize()
     assert bits_equal(out, plain)
+
+
+@pytest.mark.parametrize("grid", ["flat", "split"])
+def test_long_rows_merge_prefix_chunks_and_many_pieces(gpu, grid):
+    """Rows of ~40k keys after a 2048-key shared prefix: each has the prefix chunks' partials
+    plus its decode pieces (about 250 on the flat grid, 79 splits of 512 keys on the split
+    grid), more than one round of the combine's loads (64 partials), so the combine folds
+    several rounds that mix prefix and decode units. The 4-row batch takes the flat decode
+    grid; padded with zero-length rows past 192 it takes the split grid."""
+    lens = [2048 + 40000, 2048 + 39111, 2048 + 1000, 2048 + 38000]
+    nsh = 2048 // BS
+    priv = [math.ceil(lk / BS) - nsh for lk in lens]
+    nb = nsh + sum(priv)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(21)).tolist()
+    shared, pos, tables = perm[:nsh], nsh, []
+    for n in priv:
+        tables.append(shared + perm[pos:pos + n])
+        pos += n
+    q_lens = [1] * len(lens)
+    if grid == "split":  # graph-padding rows: zero-length sequences after the real ones
+        tables += [[-1]] * 196
+        lens += [0] * 196
+        q_lens += [0] * 196
+    b = _batch(tables, lens, q_lens, 16, 8, nb, 22, gpu)
+    print(f"[shared prefix] long rows, {grid} grid", flush=True)
+    out = _run(b, 2048, hint=2048)
+    want = _oracle(b)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, want, f"long rows, {grid} grid")
