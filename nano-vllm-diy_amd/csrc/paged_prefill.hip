@@ -25,7 +25,8 @@
 //      heads is kv head i mod 8, so a head's K/V stays in one XCD's L2), then steals from
 //      the other sub-queues. An unsplit item writes bf16 rows; a split item writes its
 //      fp32 numerators and (max, sum) per row.
-//   3. merge: combines the partials of every split unit.
+//   3. merge: combines the partials of every split unit, then the decode rows' partials
+//      left by the call's decode launch (paged_decode.hip), which needs no combine launch.
 // The split bounds the longest chain of dependent tiles (a long cached prefix would
 // otherwise keep one work-group busy long after the rest of the GPU has finished).
 //
