@@ -485,5 +485,55 @@ __device__ __forceinline__ void combine_row(const AttnArgs& a, int b, int h, int
   a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(r.z / r.y);
 }
 
+// combine_row for a split-grid batch without a shared prefix whose sequences have at most
+// max_splits <= N partials: sequence b's partials are units b * max_splits + j whatever its
+// length, so every slot's (max, sum) and element d are loaded in the same round as the
+// lengths (one memory round trip instead of two). Slots past the sequence's splits hold
+// stale or unwritten data: they are excluded by selects, never by a multiplication by zero
+// (which would let a stale NaN through).
+template <int N>
+__device__ __forceinline__ void combine_row_eager(const AttnArgs& a, int b, int h, int d) {
+  constexpr int D = kHeadDim;
+  const int H = a.num_heads;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ms = a.max_splits;  // <= N (checked by the launch)
+  const int64_t u0 = (int64_t)b * ms;
+  const uint16_t* po = a.part_o + (u0 * H + h) * D + d;
+  const int64_t stride = (int64_t)H * D;
+  const int q0 = a.cu_q[b];
+  const int q1 = a.cu_q[b + 1];
+  const int k_lo = a.cu_k[b];
+  const int k_hi = a.cu_k[b + 1];
+  const float2 mlr = *reinterpret_cast<const float2*>(a.part_ml + ((u0 + min(lane, ms - 1)) * H + h) * 2);
+  uint16_t vr[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) vr[j] = po[min(j, ms - 1) * stride];
+  // every value is consumed here, so the loads above go out together ahead of any branch
+  // (the compiler would otherwise sink each load next to its first use, behind the lengths)
+  asm volatile("" ::"v"(mlr.x), "v"(mlr.y), "s"(q0), "s"(q1), "s"(k_lo), "s"(k_hi) : "memory");
+#pragma unroll
+  for (int j = 0; j < N; ++j) asm volatile("" ::"v"(vr[j]));
+  const float2 ml = lane < ms ? mlr : make_float2(-INFINITY, 0.f);
+  float v[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = bf16_to_f32(vr[j]);
+  // No branch before the store (the compiler would sink the loads behind it): a row that is
+  // not a decode row, or that the decode kernel wrote directly (one split), is merged anyway
+  // and not stored.
+  const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
+  const int nsplit = min((max(Lk, 0) + a.split_tokens - 1) / a.split_tokens, ms);
+  const bool store = q1 - q0 == 1 && nsplit > 1;
+  const float mv = lane < nsplit ? ml.x : -INFINITY;
+  const float rm = row16_max(mv);
+  const float mx = fmaxf(fmaxf(lane_value(rm, 0), lane_value(rm, 16)), fmaxf(lane_value(rm, 32), lane_value(rm, 48)));
+  const float w = lane < nsplit ? exp2_fast(mv - mx) * ml.y : 0.f;
+  const float rs = row16_sum(w);
+  const float lsum = (lane_value(rs, 0) + lane_value(rs, 16)) + (lane_value(rs, 32) + lane_value(rs, 48));
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < N; ++j) acc = fmaf(lane_value(w, j), j < nsplit ? v[j] : 0.f, acc);
+  if (store) a.out[(int64_t)q0 * a.out_row_stride + h * D + d] = f32_to_bf16(acc / lsum);
+}
+
 }  // namespace
 }  // namespace pk

@@ -191,8 +191,23 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(con
                                   ((int64_t)a.flat_unit0 + u) * a.num_heads);
 }
 
+// EAGER > 0 (small split-grid batches without a shared prefix, max_splits <= EAGER): the
+// partial slots' loads go out with the lengths (combine_row_eager).
+template <int EAGER>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const AttnArgs a) {
-  combine_row(a, blockIdx.y, blockIdx.x, threadIdx.x);
+  if constexpr (EAGER > 0)
+    combine_row_eager<EAGER>(a, blockIdx.y, blockIdx.x, threadIdx.x);
+  else
+    combine_row(a, blockIdx.y, blockIdx.x, threadIdx.x);
+}
+
+// Small split-grid batches (at most 1024 split work-groups, no shared prefix, 17 to
+// kCombineFast splits per sequence, e.g. 8 rows of up to 2048 keys in 64-key splits): the
+// combine is a latency-bound chain of memory round trips, and its eager form takes one of
+// them off. With 16 or fewer splits it measured no faster.
+bool eager_combine(const AttnArgs& a) {
+  return a.flat_groups <= 0 && a.prefix_keys <= 0 && a.max_splits > 16 && a.max_splits <= kCombineFast &&
+         (int64_t)a.grid_splits * a.num_seqs <= 1024;
 }
 
 template <int G, int U>
@@ -284,8 +299,13 @@ hipError_t launch_decode(const AttnArgs& args, int group, bool paged, int max_se
   if (err != hipSuccess) return err;
   // (a call with prefill rows merges the decode partials in its prefill merge kernel)
   if ((a.max_splits > 1 || a.flat_groups > 0) && !a.combine_in_merge) {
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)a.num_heads, (unsigned)a.num_seqs),
-                       dim3(kCombineThreads), 0, stream, a);
+    const dim3 grid((unsigned)a.num_heads, (unsigned)a.num_seqs), block(kCombineThreads);
+    if (!eager_combine(a))
+      hipLaunchKernelGGL((decode_combine_kernel<0>), grid, block, 0, stream, a);
+    else if (a.max_splits <= 32)
+      hipLaunchKernelGGL((decode_combine_kernel<32>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_combine_kernel<kCombineFast>), grid, block, 0, stream, a);
     err = hipGetLastError();
   }
   return err;
