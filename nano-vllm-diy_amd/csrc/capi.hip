@@ -51,13 +51,12 @@ struct WorkspaceLayout {
   // chunked-prefill plan region (only when max_seqlen_q > 1)
   int64_t pf_item_cap;
   size_t pf_queue_off, pf_items_off, pf_merges_off, pf_part_o_off, pf_part_ml_off;
-  size_t sp_plan_off;
   pk::FlatDecodePlan flat;  // flat decode grid (flat.groups == 0: split grid only)
   size_t flat_meta_off;
   size_t total;
 };
 
-// [decode: partial numerators | partial (max, sum) | flat-grid record | shared-prefix plan]
+// [decode: partial numerators | partial (max, sum) | flat-grid record]
 // (empty when no sequence can have more than one split: those write their output directly).
 // Partial units: the split grid's num_seqs x max_splits (shared-prefix chunks in the first
 // slots of each sequence); with the flat grid, the shared-prefix chunks (num_seqs x
@@ -79,10 +78,6 @@ WorkspaceLayout workspace_layout(int num_seqs, int num_heads, int head_dim, int 
   if (w.flat.groups > 0) {  // the flat grid's run length and key-line positions, for the combine
     w.flat_meta_off = off;
     off += round_up(((size_t)num_seqs + 2) * sizeof(int32_t), kWorkspaceAlign);
-  }
-  if (w.max_splits > 1) {  // the shared-prefix plan: at most one item per (sequence, slot)
-    w.sp_plan_off = off;
-    off += round_up(pk::shared_prefix_plan_bytes(num_seqs, w.max_splits), kWorkspaceAlign);
   }
   if (max_seqlen_q > 1) {
     w.pf_item_cap = pk::prefill_item_cap(num_seqs, num_heads, max_seqlen_q);
@@ -378,7 +373,6 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
       a.prefix_keys = P;
       a.prefix_chunk = ck;
       a.prefix_slots = P / ck;
-      a.sp_plan = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ws.sp_plan_off);
       a.grid_splits = (max_seqlen_k - P + s - 1) / s;
       if (a.prefix_slots + a.grid_splits > a.max_splits)
         return fail(PK_ERR_HIP, "varlen_attention: shared-prefix slots %d + %d exceed %d", a.prefix_slots,

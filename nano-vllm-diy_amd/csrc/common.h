@@ -74,11 +74,7 @@ struct AttnArgs {
   int32_t prefix_slots;
   int32_t prefix_stride;        // partial units per sequence of the prefix chunk partials (chunk j of
                                 // sequence b at unit b * prefix_stride + j)
-  // Shared-prefix plan (workspace, after the decode partials): item counts per chunk
-  // (kSharedPrefixHeaderInts), then items [prefix_slots][num_seqs] of two int4 ((first member,
-  // members, keys held, 0), (block ids of the chunk)), then members [prefix_slots][num_seqs]
-  // int2 (sequence, query row) grouped by item.
-  int32_t* sp_plan;
+  int32_t sp_replicas;          // shared-prefix kernel: work-groups per window of sequences (set by its launch)
   // chunked-prefill work plan (workspace): a work item is (sequence, kv head, query tile,
   // key-tile range); items of one query tile that was split over several key ranges write
   // fp32 partials that a merge pass combines.
@@ -115,15 +111,10 @@ struct AttnArgs {
   int64_t new_v_stride;
 };
 
-// Shared-prefix decode limits: the plan groups sequences in one work-group (one thread per
-// sequence) and compares at most two block ids per chunk.
+// Shared-prefix decode limits: batches of up to this many sequences, chunks of at most two
+// cache blocks (a group's key compares two block ids).
 constexpr int kSharedPrefixMaxSeqs = 1024;
 constexpr int kSharedPrefixMaxChunkBlocks = 2;
-constexpr int kSharedPrefixHeaderInts = 256;  // >= the partial slots of any launch
-// Plan bytes: header, items (2 int4) and members (int2) for num_seqs x slots chunks.
-inline size_t shared_prefix_plan_bytes(int num_seqs, int slots) {
-  return (size_t)kSharedPrefixHeaderInts * 4 + (size_t)num_seqs * slots * (32 + 8);
-}
 
 // Prefill plan sizes. The kernel runs kPrefillSlotsMax persistent work-groups at most (one
 // per CU on a 256-CU part). The split size T is at least 2/3 x total work / slots, and

@@ -887,124 +887,38 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
 
 // ---- Shared-prefix decode ------------------------------------------------------------------
 // Decode rows (one query row per sequence) over keys [0, Pb), Pb = min(prefix_keys, Lk), in
-// chunks of prefix_chunk keys (one or two whole cache blocks). The sequences whose block
-// tables name the same blocks for a chunk, and that hold the same number of keys in it, form
-// a group -- with prefix caching, the sequences sharing those blocks. Work item = (chunk, up
-// to kPrefillRows / G members of a group); with kv head g it is one work unit: the members'
-// query rows (members x the G heads of g) form one MFMA tile set, so each shared block is
-// read once instead of once per sequence. Every row gets the chunk's (max, sum, numerator)
-// partial in the chunk's slot of its sequence, merged with the sequence's split partials by
-// the decode combine. A row's arithmetic does not depend on which other rows share its
-// tiles, so results do not depend on the grouping (shared or duplicated blocks give
-// identical bits) nor on the order in which the plan lists items.
-constexpr int kSpPlanThreads = kSharedPrefixMaxSeqs;
-
-// Exclusive prefix sum over the work-group (one value per thread) and the total.
-__device__ __forceinline__ int2 plan_scan(int v, int* s_w) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_up(x, o, kWave);
-    if (lane >= o) x += y;
-  }
-  if (lane == kWave - 1) s_w[wave] = x;
-  __syncthreads();
-  int off = 0, tot = 0;
-  for (int w = 0; w < kSpPlanThreads / kWave; ++w) {
-    const int c = s_w[w];
-    off += w < wave ? c : 0;
-    tot += c;
-  }
-  __syncthreads();
-  return make_int2(off + x - v, tot);
-}
-
-// One work-group per chunk, thread b = sequence b. A sequence's chunk key is (keys held, first
-// block id, second block id); sequences with equal keys form a group, found through an LDS
-// hash table on the first block id (the first sequence to claim an entry leads the group).
-// Ranks inside a group come from an atomic counter, so the member order may change from run
-// to run -- which does not change any result (see above). Members are laid out group after
-// group; every member whose rank is a multiple of the item size starts an item.
-constexpr int kPlanHash = 2 * kSharedPrefixMaxSeqs;  // entries (more than sequences: probing ends)
-
-template <int G>
-__global__ __launch_bounds__(kSpPlanThreads) void prefix_plan_kernel(const AttnArgs a) {
-  constexpr int MC = kPrefillRows / G;
-  __shared__ int s_cnt[kSpPlanThreads], s_id0[kSpPlanThreads], s_id1[kSpPlanThreads], s_size[kSpPlanThreads],
-      s_base[kSpPlanThreads], s_tab[kPlanHash];
-  __shared__ int s_w[kSpPlanThreads / kWave];
-  __shared__ int s_items;
-  const int b = threadIdx.x;
-  const int c = blockIdx.x;
-  const int S = a.num_seqs;
-  const int BS = a.block_size;
-  const int CK = a.prefix_chunk;
-  const int Cb = CK / BS;
-  int cnt = 0, q0 = 0, id0 = -1, id1 = -1;
-  if (b < S) {
-    q0 = a.cu_q[b];
-    const int Lq = a.cu_q[b + 1] - q0;
-    const int Lk = min(a.cu_k[b + 1] - a.cu_k[b], a.max_seqlen_k);
-    if (Lq == 1) cnt = max(0, min(CK, min(a.prefix_keys, Lk) - c * CK));  // decode rows only
-    if (cnt > 0) {
-      const int32_t* bt = a.block_table + (int64_t)b * a.bt_stride + c * Cb;
-      id0 = bt[0];
-      if (Cb > 1 && cnt > BS) id1 = bt[1];
-    }
-  }
-  s_cnt[b] = cnt;
-  s_id0[b] = id0;
-  s_id1[b] = id1;
-  s_size[b] = 0;
-  for (int e = b; e < kPlanHash; e += kSpPlanThreads) s_tab[e] = -1;
-  if (b == 0) s_items = 0;
-  __syncthreads();
-  int lead = -1, rank = 0;
-  if (cnt > 0) {
-    int h = (int)(((uint32_t)id0 * 2654435761u) >> 21) & (kPlanHash - 1);
-    for (int probe = 0; probe < kPlanHash; ++probe, h = (h + 1) & (kPlanHash - 1)) {
-      const int e = atomicCAS(&s_tab[h], -1, b);
-      if (e == -1) {
-        lead = b;
-        break;
-      }
-      if (s_cnt[e] == cnt && s_id0[e] == id0 && s_id1[e] == id1) {
-        lead = e;
-        break;
-      }
-    }
-    if (lead >= 0) rank = atomicAdd(&s_size[lead], 1);
-  }
-  __syncthreads();
-  // s_size[x]: the size of the group x leads (0 if x leads none)
-  s_base[b] = plan_scan(s_size[b], s_w).x;  // the group's first position in the member list
-  __syncthreads();
-  int4* items = reinterpret_cast<int4*>(a.sp_plan + kSharedPrefixHeaderInts) + (int64_t)c * S * 2;
-  int2* members = reinterpret_cast<int2*>(a.sp_plan + kSharedPrefixHeaderInts + (int64_t)a.prefix_slots * S * 8) +
-                  (int64_t)c * S;
-  if (lead >= 0) {
-    const int pos = s_base[lead] + rank;
-    members[pos] = make_int2(b, q0);
-    if (rank % MC == 0) {
-      const int idx = atomicAdd(&s_items, 1);
-      items[2 * idx] = make_int4(pos, min(MC, s_size[lead] - rank), cnt, 0);
-      items[2 * idx + 1] = make_int4(id0, id1 >= 0 ? id1 : id0, 0, 0);
-    }
-  }
-  __syncthreads();
-  if (b == 0) a.sp_plan[c] = s_items;
-}
-
+// chunks of prefix_chunk keys (one or two whole cache blocks). Work-group (chunk c, kv head g,
+// z) serves window z / R of MC = kPrefillRows / G consecutive sequences, as replica z % R. The
+// window's sequences whose block tables name the same blocks for the chunk, and that hold the
+// same number of keys in it, form a group -- with prefix caching, the sequences sharing those
+// blocks; replica r takes the window's groups r, r + R, ... A group's query rows (members x
+// the G heads of g) form one MFMA tile set, so each shared block is read once per window
+// instead of once per sequence. Every row gets the chunk's (max, sum, numerator) partial in
+// the chunk's slot of its sequence, merged with the sequence's split partials by the decode
+// combine. A row's arithmetic does not depend on which other rows share its tiles, so results
+// do not depend on the grouping (shared or duplicated blocks give identical bits) nor on the
+// order of the members inside a group.
+//
+// The grouping runs in each work-group, on its own window (no plan launch, no plan in memory):
+// thread t < MC holds sequence s0 + t's key (keys held in the chunk, its block ids), inserts it
+// into an LDS hash table and counts itself into its entry; a group's lead is its lowest
+// sequence (an atomic minimum: the same in every replica), and the groups are numbered by their
+// leads in sequence order, so all replicas of a window see the same group list. Member ranks
+// come from an atomic counter; they only place the rows inside the work-group's own tiles.
 template <int G>
 __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_kernel(const AttnArgs a) {
   static_assert(kRowBlocks == 1, "one 32-row block per wavefront");
   constexpr int D = kHeadDim;
-  constexpr int MC = kPrefillRows / G;  // member sequences per item
+  constexpr int MC = kPrefillRows / G;  // sequences per window (and rows of one head per tile set)
+  constexpr int kHash = 2 * MC;         // hash entries: more than keys, so probing ends
+  static_assert(MC <= kPrefillThreads, "one thread per window sequence");
   __shared__ __attribute__((aligned(1024))) char sK[2][kTileBytes];
   __shared__ __attribute__((aligned(1024))) char sV[2][kTileBytes];
-  __shared__ int2 s_mem[MC];  // (sequence, query row)
+  __shared__ int4 s_key[MC];   // (keys held in the chunk, block id, second block id or -1, query row)
+  __shared__ int s_owner[kHash], s_lead[kHash], s_size[kHash];
+  __shared__ int2 s_group[MC];  // group k: (lead, members)
+  __shared__ int s_wave_leads[kPrefillWaves];
+  __shared__ int2 s_mem[MC];    // (sequence, query row) of the current group's members
   lds_char* KS[2] = {(lds_char*)sK[0], (lds_char*)sK[1]};
   lds_char* VS[2] = {(lds_char*)sV[0], (lds_char*)sV[1]};
 
@@ -1015,35 +929,81 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
   const int CK = a.prefix_chunk;
   const int Cb = CK / BS;
   const int S = a.num_seqs;
-  // grid (chunk, kv head, worker): work-groups go to the XCDs round-robin by linear id, so
-  // with the worker slowest the first (busiest) worker of every (chunk, head) spreads over
-  // all of them
+  // grid (chunk, kv head, window x replicas): work-groups go to the XCDs round-robin by linear
+  // id, so with z slowest the first replica of every (chunk, head) spreads over all of them
   const int c = blockIdx.x;
   const int g = blockIdx.y;
-  const int4* items = reinterpret_cast<const int4*>(a.sp_plan + kSharedPrefixHeaderInts) + (int64_t)c * S * 2;
-  // this worker's first item is read together with the chunk's item count (the slot lies in
-  // the chunk's item list, blockIdx.z < num_seqs; it is used only if the count covers it)
-  int4 it = items[2 * blockIdx.z];
-  int4 ids = items[2 * blockIdx.z + 1];
-  const int n_items = min(a.sp_plan[c], S);
-  const int2* members =
-      reinterpret_cast<const int2*>(a.sp_plan + kSharedPrefixHeaderInts + (int64_t)a.prefix_slots * S * 8) +
-      (int64_t)c * S;
+  const int nrep = a.sp_replicas;
+  const int win = (int)blockIdx.z / nrep;
+  const int rep = (int)blockIdx.z - win * nrep;
+  const int s0 = win * MC;
+  const int nwin = min(MC, S - s0);
+
+  // the window's bounds and block-table entries for the chunk in one round of loads (the
+  // entries, clamped into the table row, are used only for a sequence holding keys in the
+  // chunk, whose entries are valid)
+  int4 key = make_int4(0, -1, -1, 0);
+  if (tid < nwin) {
+    const int b = s0 + tid;
+    const int32_t* bt = a.block_table + (int64_t)b * a.bt_stride;
+    const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
+    const int k_lo = a.cu_k[b], k_hi = a.cu_k[b + 1];
+    const int id0 = bt[min(c * Cb, a.bt_stride - 1)];
+    const int id1 = Cb > 1 ? bt[min(c * Cb + 1, a.bt_stride - 1)] : -1;
+    const int Lk = min(k_hi - k_lo, a.max_seqlen_k);
+    const int cnt = q1 - q0 == 1 ? max(0, min(CK, min(a.prefix_keys, Lk) - c * CK)) : 0;  // decode rows only
+    if (cnt > 0) key = make_int4(cnt, id0, cnt > BS ? id1 : -1, q0);
+  }
+  if (tid < MC) s_key[tid] = key;
+  for (int e = tid; e < kHash; e += kPrefillThreads) {
+    s_owner[e] = -1;
+    s_lead[e] = MC;
+    s_size[e] = 0;
+  }
+  __syncthreads();
+  int slot = -1, rank = 0;
+  if (key.x > 0) {
+    int h = (int)(((uint32_t)key.y * 2654435761u + (uint32_t)key.z * 40503u) >> 16) & (kHash - 1);
+    for (int probe = 0; probe < kHash; ++probe, h = (h + 1) & (kHash - 1)) {
+      const int e = atomicCAS(&s_owner[h], -1, tid);
+      const int4 k2 = e == -1 ? key : s_key[e];
+      if (k2.x == key.x && k2.y == key.y && k2.z == key.z) {
+        slot = h;
+        break;
+      }
+    }
+    if (slot >= 0) {
+      atomicMin(&s_lead[slot], tid);
+      rank = atomicAdd(&s_size[slot], 1);
+    }
+  }
+  __syncthreads();
+  const int my_lead = slot >= 0 ? s_lead[slot] : -1;
+  // group number of a lead: leads below it, in sequence order (ballots per wavefront)
+  const bool is_lead = my_lead == tid;
+  const uint64_t lead_bits = __builtin_amdgcn_ballot_w64(is_lead);
+  if (lane == 0) s_wave_leads[wave] = __builtin_popcountll(lead_bits);
+  __syncthreads();
+  int before = __builtin_popcountll(lead_bits & ((1ull << lane) - 1ull)), ngroups = 0;
+#pragma unroll
+  for (int w = 0; w < kPrefillWaves; ++w) {
+    const int n = s_wave_leads[w];
+    before += w < wave ? n : 0;
+    ngroups += n;
+  }
+  if (is_lead) s_group[before] = make_int2(tid, s_size[slot]);
+  __syncthreads();
+
   const TileLanes tl = tile_lanes(lane);
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  for (int i = blockIdx.z; i < n_items; i += gridDim.z) {
-    if (i != (int)blockIdx.z) {
-      it = items[2 * i];
-      ids = items[2 * i + 1];
-    }
-    const int nmem = min(it.y, MC);
-    const int cnt = it.z;
-    const int id0 = ids.x, id1 = ids.y;
-    // the plan is trusted only as far as the buffers reach (see prefill_item)
-    if (it.x < 0 || nmem <= 0 || it.x + nmem > S || cnt <= 0 || cnt > CK || (cnt > BS && Cb < 2)) continue;
-
+  for (int k = rep; k < ngroups; k += nrep) {
+    const int2 grp = s_group[k];
+    const int4 gkey = s_key[grp.x];
+    const int nmem = grp.y;
+    const int cnt = gkey.x;
+    const int id0 = gkey.y, id1 = gkey.z >= 0 ? gkey.z : gkey.y;
     // tile n: keys 64 n .. of the chunk, in its block (64 n) / BS; rows past cnt re-read the
     // chunk's last key (same block) and are masked
     const auto load = [&](int n, KvRegs& R) {
@@ -1065,8 +1025,8 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
     KvRegs R0, R;
     load(0, R0);
     if (ntiles > 1) load(1, R);
-    __syncthreads();  // s_mem of the previous item has been read
-    if (tid < nmem) s_mem[tid] = members[it.x + tid];
+    __syncthreads();  // s_mem of the previous group has been read
+    if (my_lead == grp.x) s_mem[rank] = make_int2(s0 + tid, key.w);
     __syncthreads();
 
     // rows: 32 per wavefront; TMd = members rounded up to 32 rows per head, head i = row / TMd
@@ -1133,6 +1093,7 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
   }
 }
 
+
 int device_prefill_slots() {
   static int cached[64];
   int dev = 0;
@@ -1169,21 +1130,25 @@ hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_
 }  // namespace
 
 template <int G>
-void launch_shared_prefix_g(const AttnArgs& a, hipStream_t stream) {
-  // plan: one work-group per chunk; items: (chunk, kv head, worker), the workers of a chunk
-  // taking its items in turn, sized so the grid holds about two work-groups per CU
+void launch_shared_prefix_g(AttnArgs a, hipStream_t stream) {
+  // grid (chunk, kv head, window x replicas): windows of kPrefillRows / G sequences, and
+  // replicas taking a window's groups in turn, as many as keep the grid near two work-groups
+  // per CU (a window usually holds one group per chunk; the spare replicas exit after the
+  // grouping)
+  constexpr int MC = kPrefillRows / G;
+  const int windows = (a.num_seqs + MC - 1) / MC;
   const int pool = 2 * device_prefill_slots();
-  const int workers = std::max(1, std::min(a.num_seqs, pool / std::max(1, a.prefix_slots * a.num_kv_heads)));
-  hipLaunchKernelGGL(prefix_plan_kernel<G>, dim3((unsigned)a.prefix_slots), dim3(kSpPlanThreads), 0, stream, a);
-  hipLaunchKernelGGL(shared_prefix_kernel<G>, dim3((unsigned)a.prefix_slots, (unsigned)a.num_kv_heads, (unsigned)workers),
+  a.sp_replicas = std::max(1, std::min(MC, pool / std::max(1, a.prefix_slots * a.num_kv_heads * windows)));
+  hipLaunchKernelGGL(shared_prefix_kernel<G>,
+                     dim3((unsigned)a.prefix_slots, (unsigned)a.num_kv_heads, (unsigned)(windows * a.sp_replicas)),
                      dim3(kPrefillThreads), 0, stream, a);
 }
 
 hipError_t launch_shared_prefix(const AttnArgs& a, int group, hipStream_t stream) {
   if (a.num_seqs <= 0 || a.prefix_keys <= 0 || a.prefix_slots <= 0) return hipSuccess;
-  if (!a.block_table || !a.part_o || !a.part_ml || !a.sp_plan || a.num_seqs > kSharedPrefixMaxSeqs ||
+  if (!a.block_table || !a.part_o || !a.part_ml || a.num_seqs > kSharedPrefixMaxSeqs ||
       a.prefix_chunk % a.block_size != 0 || a.prefix_chunk / a.block_size > kSharedPrefixMaxChunkBlocks ||
-      a.prefix_slots > kSharedPrefixHeaderInts)
+      a.prefix_slots > kCombineMaxSplits)
     return hipErrorInvalidValue;
   switch (group) {
     case 1: launch_shared_prefix_g<1>(a, stream); break;

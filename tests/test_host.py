@@ -82,9 +82,6 @@ def test_workspace_size_formula():
     units = 256 * (8192 // split) * HQ
     want = math.ceil(units * HEAD_DIM * 2 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
     # (bf16 outputs and fp32 (max, sum) per partial unit and head)
-    # + the shared-prefix plan: item counts per chunk (1 KiB), then per (sequence, slot) one
-    # item (32 B) and one member (8 B)
-    want += math.ceil((1024 + 256 * (8192 // split) * 40) / 256) * 256
     assert ws == want
     # 128 sequences of <= 2048 keys take the flat decode grid: 896 runs of keys + 128
     # sequences, one partial unit each, after room for shared-prefix chunks (at most the split
@@ -94,7 +91,6 @@ def test_workspace_size_formula():
     units = (128 * (2048 // 128) + 128 + 896) * HQ
     want = math.ceil(units * HEAD_DIM * 2 / 256) * 256 + math.ceil(units * 2 * 4 / 256) * 256
     want += math.ceil(130 * 4 / 256) * 256
-    want += math.ceil((1024 + 128 * (2048 // 128) * 40) / 256) * 256
     assert ws == want
 
 
