@@ -1025,9 +1025,10 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
     KvRegs R0, R;
     load(0, R0);
     if (ntiles > 1) load(1, R);
-    __syncthreads();  // s_mem of the previous group has been read
+    // LDS-only barriers: __syncthreads() would also wait for the tile loads just issued
+    lds_barrier();  // s_mem of the previous group has been read
     if (my_lead == grp.x) s_mem[rank] = make_int2(s0 + tid, key.w);
-    __syncthreads();
+    lds_barrier();
 
     // rows: 32 per wavefront; TMd = members rounded up to 32 rows per head, head i = row / TMd
     const int TMd = (nmem + 31) & ~31;
