@@ -220,3 +220,27 @@ def test_long_rows_merge_prefix_chunks_and_many_pieces(gpu, grid):
     want = _oracle(b)
     torch.cuda.synchronize()
     assert_close_bf16(out, want, f"long rows, {grid} grid")
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (16, 2)])
+def test_work_groups_take_several_groups_in_turn(gpu, hq, hkv):
+    """256 sequences in six prefix groups (sequence b shares the 8 prefix blocks of group
+    b mod 6), one private block each: every window of sequences (128 for GQA 2, 32 for GQA 8)
+    holds all six groups, and the grid has 4 work-groups per window and chunk, so some take
+    two groups in turn (reusing their member list and tile stages)."""
+    nsh, ngrp, n = 8, 6, 256
+    tables, lens = [], []
+    nxt = ngrp * nsh
+    for b in range(n):
+        g = b % ngrp
+        tables.append(list(range(g * nsh, (g + 1) * nsh)) + [nxt])
+        nxt += 1
+        lens.append(nsh * BS + 1 + (b * 37) % (BS - 1))
+    b = _batch(tables, lens, [1] * n, hq, hkv, nxt, seed=31 + hkv, dev=gpu)
+    print(f"[shared prefix] several groups per work-group, hq={hq} hkv={hkv}", flush=True)
+    out = _run(b, nsh * BS, hint=nsh * BS)
+    plain = _run(b, None, hint=nsh * BS)
+    want = _oracle(b)
+    torch.cuda.synchronize()
+    assert_close_bf16(out, want, f"six groups per window, hkv={hkv}")
+    assert_close_bf16(plain, want, f"plain path, hkv={hkv}")
