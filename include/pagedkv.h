@@ -166,7 +166,8 @@ int pk_varlen_attention_ex(const void* q, int64_t q_row_stride,
  *     whole chunks of lcm(block_size, the decode split) keys, are processed in chunks: the
  *     sequences whose block tables name the same blocks for a chunk (and hold the same number
  *     of keys in it) put their query rows into one set of bf16 MFMA tiles, so each shared
- *     block is read once; the keys past P go through the split-K decode kernel, and the
+ *     block is read once per kv head and window of 256 / (num_heads / num_kv_heads)
+ *     consecutive sequences; the keys past P go through the split-K decode kernel, and the
  *     combine merges both. Sequences that share nothing are still correct (a group of one).
  *     0 is pk_varlen_attention_ex. Paged mode only; prefill rows (Lq > 1) are unaffected.
  *   Results: within the attention tolerance of pk_varlen_attention_ex (the prefix is summed
