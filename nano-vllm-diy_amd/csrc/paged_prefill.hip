@@ -474,7 +474,9 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const AttnAr
       }
     }
   }
-  __syncthreads();
+  // LDS-only: the counts in cur are final; the work-list stores need not complete before the
+  // queue header's (the prefill kernel, a later launch, reads both)
+  lds_barrier();
   if (tid < 8) a.pf_queue[tid * kPrefillQueueStride] = 0;
   if (tid == 0) {
     a.pf_queue[kPrefillQueueMeta] = (int)(min((int64_t)tot, (int64_t)a.pf_item_cap) * hkv);
