@@ -222,6 +222,7 @@ def cpu_baselines(dev, gpu_kernels: dict | None, reps: int = 3) -> dict:
     sec = cpu_oracle_time(w4, list(range(len(w4.q_lens))), reps)
     entry("cfg4_decode", sec, w4.decode_kv_bytes(), "GB/s", "cfg4_decode", "logical_GB/s")
     res["cfg4_decode"]["unique_GB/s"] = round(w4.decode_unique_kv_bytes() / sec / 1e9, 3)
+    res["cfg4_decode"]["unique_block_GB/s"] = round(w4.decode_unique_block_bytes() / sec / 1e9, 3)
     return res
 
 
@@ -466,6 +467,68 @@ def producer_call(dev, n: int, seed: int = 6):
     return fn, n * per_token
 
 
+def store_call(dev, n: int, seed: int = 8):
+    """store_kvcache of n new tokens as a prefill step of the serving engine issues it: k
+    contiguous, v the strided view of the fused qkv row (row stride 4096 elements,
+    qwen3.py:80-88), slots filling whole cache blocks popped from a shuffled pool. Bytes:
+    4 n R + 4 n (read K and V rows, write them, read the slot)."""
+    import torch
+
+    import pagedkv
+    from pagedkv.workloads import BLOCK_SIZE, HEAD_DIM, HKV, HQ, ROW_BYTES
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    qkv = torch.randn(n, (HQ + 2 * HKV) * HEAD_DIM, generator=g, device=dev).to(torch.bfloat16)
+    k = qkv[:, HQ * HEAD_DIM:(HQ + HKV) * HEAD_DIM].reshape(n, HKV, HEAD_DIM).clone()
+    v = qkv[:, (HQ + HKV) * HEAD_DIM:].view(n, HKV, HEAD_DIM)
+    nb = 2 * ((n + BLOCK_SIZE - 1) // BLOCK_SIZE)
+    blocks = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))[:nb // 2]
+    slots = (blocks.repeat_interleave(BLOCK_SIZE) * BLOCK_SIZE +
+             torch.arange(BLOCK_SIZE).repeat(nb // 2))[:n].to(torch.int32).to(dev)
+    kc = torch.empty(nb, BLOCK_SIZE, HKV, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+
+    def fn():
+        pagedkv.store_kvcache(k, v, kc, vc, slots)
+    return fn, 4 * n * ROW_BYTES + 4 * n
+
+
+def dense_prefill_call(dev, seed: int = 5, budget: int = 16384):
+    """The serving run's first prefill step in dense (flat) mode, as the reference runs a
+    batch of fresh prompts (block_tables None, cu_seqlens_k == cu_seqlens_q,
+    model_runner.py:211-212): the first prompts of the serving workload up to the
+    16384-token budget, the last one cut to fit (a chunk with no cached keys is still
+    fresh). q (N, 16, 128), k contiguous, v the strided qkv view. Returns the call, its
+    causal flops and the prompt lengths."""
+    import itertools
+
+    import torch
+
+    import pagedkv
+    from pagedkv.workloads import HEAD_DIM, HKV, HQ, serving_requests
+
+    prompts, _ = serving_requests(seed, 256)
+    lens, tot = [], 0
+    for p in prompts:
+        take = min(len(p), budget - tot)
+        if take <= 0:
+            break
+        lens.append(take)
+        tot += take
+    g = torch.Generator(device=dev).manual_seed(seed)
+    qkv = torch.randn(tot, (HQ + 2 * HKV) * HEAD_DIM, generator=g, device=dev).to(torch.bfloat16)
+    q = qkv[:, :HQ * HEAD_DIM].reshape(tot, HQ, HEAD_DIM).clone()
+    k = qkv[:, HQ * HEAD_DIM:(HQ + HKV) * HEAD_DIM].reshape(tot, HKV, HEAD_DIM).clone()
+    v = qkv[:, (HQ + HKV) * HEAD_DIM:].view(tot, HKV, HEAD_DIM)
+    cu = torch.tensor([0, *itertools.accumulate(lens)], dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    flops = sum(4 * HQ * HEAD_DIM * (lq * (lq + 1) // 2) for lq in lens)
+
+    def fn():
+        pagedkv.varlen_attention(q, k, v, cu, cu, max(lens), max(lens), SCALE, True, None, out=out)
+    return fn, flops, lens
+
+
 def linear_calls(dev, rows: int, seed: int = 7):
     """The four decode-step projections of one Qwen3-0.6B decoder layer on `rows` tokens,
     each with its fused epilogue: qkv (store), o + residual RMSNorm, gate/up + SiLU * mul,
@@ -509,6 +572,12 @@ def extra_configs(dev, w2):
     res["cache_state"] = "cold: 512 MiB read before every timed launch"
     res["cfg2_store"] = {"ms": round(ms, 5), "GB/s": round(w2.store_bytes() / ms / 1e6, 1)}
 
+    # the store at a prefill step's size (the serving run's 16384-token budget)
+    fn, nbytes = store_call(dev, 16384)
+    ms, _ = timed_launches(fn, 20)
+    res["store_16384"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+                          "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
     log("[bench] cfg1")
     ws = make_workload("cfg1_store", dev)
     ms, _ = timed_launches(lambda: pagedkv.store_kvcache(ws.k, ws.v, ws.k_cache, ws.v_cache, ws.slot_mapping), 20)
@@ -542,6 +611,25 @@ def extra_configs(dev, w2):
     kvb = w3.decode_kv_bytes()
     res["cfg3_decode"] = {"ms": round(ms_d, 5), "GB/s": round(kvb / ms_d / 1e6, 1), "seqs": n_dec}
 
+    fn, fl_d, lens = dense_prefill_call(dev)
+    ms_dp, _ = timed_launches(fn, 20)
+    res["dense_prefill_16384"] = {"ms": round(ms_dp, 5), "TFLOP/s": round(fl_d / ms_dp / 1e9, 2),
+                                  "mfma_frac": round(fl_d / ms_dp / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+                                  "flops": fl_d, "batch": f"{len(lens)} fresh prompts, {sum(lens)} tokens "
+                                  "(the serving run's first prefill step), flat K/V, causal"}
+
+    log("[bench] decode at one tensor-parallel rank's share of the heads")
+    from pagedkv.workloads import TP_HEADS
+    for tp in (2, 4, 8):
+        hq, hkv = TP_HEADS[tp]
+        wt = make_workload("cfg2", dev, heads=(hq, hkv))
+        ms, _ = timed_launches(attention_call(wt), 20)
+        gbs = wt.decode_kv_bytes() / ms / 1e6
+        res[f"cfg2_tp{tp}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                               "heads": f"{hq}q/{hkv}kv", "kv_bytes": wt.decode_kv_bytes()}
+        del wt
+        torch.cuda.empty_cache()
+
     log("[bench] producer")
     for n in (256, 16384):
         fn, nbytes = producer_call(dev, n)
@@ -560,13 +648,23 @@ def extra_configs(dev, w2):
     log("[bench] cfg4")
     w4 = make_workload("cfg4", dev)
     ms, _ = timed_launches(attention_call(w4), 20)
-    res["cfg4_decode"] = {"ms": round(ms, 5), "logical_GB/s": round(w4.decode_kv_bytes() / ms / 1e6, 1),
-                          "unique_GB/s": round(w4.decode_unique_kv_bytes() / ms / 1e6, 1),
-                          "path": "shared-prefix decode (the 8 shared blocks once, on MFMA) + split-K suffix"}
+    # unique: (2048 + sum of the suffixes) * 2R, the distinct keys; unique_block: the distinct
+    # cache blocks read, whole; logical: sum Lk * 2R, every sequence's keys
+    cfg4_bytes = {"unique": w4.decode_unique_kv_bytes(), "unique_block": w4.decode_unique_block_bytes(),
+                  "logical": w4.decode_kv_bytes()}
+
+    def cfg4_entry(ms, path):
+        e = {"ms": round(ms, 5)}
+        for k, b in cfg4_bytes.items():
+            e[f"{k}_GB/s"] = round(b / ms / 1e6, 1)
+        e["unique_frac"] = round(cfg4_bytes["unique"] / ms / 1e6 / HBM_PEAK_GBS, 4)
+        e["path"] = path
+        return e
+    res["cfg4_decode"] = cfg4_entry(ms, "shared-prefix decode (the 8 shared blocks once per kv head, on MFMA) "
+                                        "+ flat grid over the suffixes")
     ms, _ = timed_launches(attention_call(w4, shared=False), 20)
-    res["cfg4_decode_plain"] = {"ms": round(ms, 5), "logical_GB/s": round(w4.decode_kv_bytes() / ms / 1e6, 1),
-                                "unique_GB/s": round(w4.decode_unique_kv_bytes() / ms / 1e6, 1),
-                                "path": "split-K over every key of every sequence"}
+    res["cfg4_decode_plain"] = cfg4_entry(ms, "split-K over every key of every sequence")
+    res["cfg4_bytes"] = cfg4_bytes
     return res
 
 

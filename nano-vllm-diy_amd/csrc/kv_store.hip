@@ -4,35 +4,60 @@
 // program per token and copies the token's K row and V row (num_kv_heads * head_dim
 // elements each) into slot slot_mapping[i], skipping slot -1.
 //
-// Here a thread moves one 16-byte chunk of a K row and the matching chunk of the V
-// row, so a wavefront stores 1 KiB of contiguous cache row per operand with
-// dwordx4 stores and many tokens are in flight per work-group. The copy is a bit
-// copy: results are identical to the reference for any 16-bit dtype.
+// Here a work-group moves the rows of a few consecutive tokens (8 tokens of a 2 KiB
+// row): a thread moves four 16-byte chunks of K rows and the matching chunks of the V
+// rows, so a wavefront stores 1 KiB of contiguous cache row per operand and
+// instruction, with dwordx4 stores. The copy is a bit copy: results are identical to
+// the reference for any 16-bit dtype.
 #include "common.h"
 
 namespace pk {
 namespace {
 
 constexpr int kStoreThreads = 256;
+constexpr int kStoreUnroll = 4;  // 16-byte chunks per thread and round, loads issued together
+constexpr int kStoreChunks = kStoreThreads * kStoreUnroll;  // chunks a work-group moves per round
 
+// Work-group x moves tokens [x * tokens_per_group, ...): its chunks are numbered i = token
+// offset * row_vec + chunk, and a round gives thread j chunks j, j + 256, j + 512, j + 768.
+// The token of chunk i is i >> row_shift when the row is a power of two of chunks (every
+// head geometry with a power-of-two kv head count and head_dim 128), else a 32-bit
+// division. All slot loads of a round go out first, then all K and V loads (from a valid
+// row even where the slot is -1, so no load waits behind a branch), then the stores.
 __global__ __launch_bounds__(kStoreThreads) void store_kvcache_kernel(
     const uint4* __restrict__ key, int64_t key_row_vec, const uint4* __restrict__ value,
     int64_t value_row_vec, uint4* __restrict__ k_cache, uint4* __restrict__ v_cache,
-    const int32_t* __restrict__ slot_mapping, int32_t num_tokens, int32_t row_vec,
-    int64_t num_slots) {
-  const int64_t total = (int64_t)num_tokens * row_vec;
-  const int64_t step = (int64_t)gridDim.x * kStoreThreads;
-  for (int64_t idx = (int64_t)blockIdx.x * kStoreThreads + threadIdx.x; idx < total; idx += step) {
-    const int32_t token = (int32_t)(idx / row_vec);
-    const int32_t chunk = (int32_t)(idx - (int64_t)token * row_vec);
-    const int32_t slot = slot_mapping[token];
-    if (slot == -1) continue;                                        // attention.py:23
-    if (num_slots > 0 && (slot < 0 || (int64_t)slot >= num_slots)) continue;  // opt-in bound check
-    const uint4 kv = key[(int64_t)token * key_row_vec + chunk];
-    const uint4 vv = value[(int64_t)token * value_row_vec + chunk];
-    const int64_t dst = (int64_t)slot * row_vec + chunk;
-    k_cache[dst] = kv;
-    v_cache[dst] = vv;
+    const int32_t* __restrict__ slot_mapping, int32_t num_tokens, int32_t row_vec, int32_t row_shift,
+    int32_t tokens_per_group, int64_t num_slots) {
+  const int32_t t0 = blockIdx.x * tokens_per_group;
+  const int32_t n = min(tokens_per_group, num_tokens - t0) * row_vec;  // chunks of this work-group
+  for (int32_t base = 0; base < n; base += kStoreChunks) {
+    int32_t tok[kStoreUnroll], chunk[kStoreUnroll], slot[kStoreUnroll];
+#pragma unroll
+    for (int j = 0; j < kStoreUnroll; ++j) {
+      const int32_t i = min(base + j * kStoreThreads + (int32_t)threadIdx.x, n - 1);
+      const int32_t t = row_shift >= 0 ? i >> row_shift : i / row_vec;
+      tok[j] = t0 + t;
+      chunk[j] = i - t * row_vec;
+      slot[j] = slot_mapping[tok[j]];
+    }
+    uint4 kv[kStoreUnroll], vv[kStoreUnroll];
+#pragma unroll
+    for (int j = 0; j < kStoreUnroll; ++j) {
+      kv[j] = key[(int64_t)tok[j] * key_row_vec + chunk[j]];
+      vv[j] = value[(int64_t)tok[j] * value_row_vec + chunk[j]];
+    }
+#pragma unroll
+    for (int j = 0; j < kStoreUnroll; ++j) {
+      const int32_t s = slot[j];
+      const bool live = base + j * kStoreThreads + (int32_t)threadIdx.x < n && s != -1 &&  // attention.py:23
+                        (num_slots <= 0 || (s >= 0 && (int64_t)s < num_slots));          // opt-in bound check
+      if (live) {
+        const int64_t dst = (int64_t)s * row_vec + chunk[j];
+        k_cache[dst] = kv[j];
+        v_cache[dst] = vv[j];
+      }
+    }
   }
 }
 
@@ -65,14 +90,16 @@ hipError_t launch_store_kvcache(const void* key, int64_t key_row_stride, const v
                                 int32_t row_elems, int64_t num_slots, hipStream_t stream) {
   if (num_tokens <= 0) return hipSuccess;
   const int32_t row_vec = row_elems / 8;
-  const int64_t total = (int64_t)num_tokens * row_vec;
-  int64_t blocks = (total + kStoreThreads - 1) / kStoreThreads;
-  if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(store_kvcache_kernel, dim3((unsigned)blocks), dim3(kStoreThreads), 0, stream,
+  int32_t row_shift = -1;
+  if ((row_vec & (row_vec - 1)) == 0) row_shift = __builtin_ctz((unsigned)row_vec);
+  // one round of 1024 chunks per work-group (8 tokens of a 2 KiB row), at least one token
+  const int32_t per_group = row_vec >= kStoreChunks ? 1 : kStoreChunks / row_vec;
+  const int64_t groups = ((int64_t)num_tokens + per_group - 1) / per_group;
+  hipLaunchKernelGGL(store_kvcache_kernel, dim3((unsigned)groups), dim3(kStoreThreads), 0, stream,
                      static_cast<const uint4*>(key), key_row_stride / 8,
                      static_cast<const uint4*>(value), value_row_stride / 8,
                      static_cast<uint4*>(k_cache), static_cast<uint4*>(v_cache), slot_mapping,
-                     num_tokens, row_vec, num_slots);
+                     num_tokens, row_vec, row_shift, per_group, num_slots);
   return hipGetLastError();
 }
 

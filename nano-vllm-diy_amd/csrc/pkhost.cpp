@@ -158,8 +158,9 @@ struct pkh_engine {
     // prefill (:64-110)
     while (!prefill.empty() && (int32_t)scheduled.size() < cfg.max_num_seqs) {
       Seq* s = prefill.front();
-      // hit-free prefix lookup: the cached count drops to its block boundary (:318),
-      // restored when the sequence is not scheduled this step (:320-337)
+      // hit-free prefix lookup: the cached count drops to its block boundary
+      // (block_manager.py:158), restored when the sequence is not scheduled this step (the
+      // undo closure, block_manager.py:160-177)
       const int32_t prev_cached = s->num_cached;
       s->num_cached = s->num_cached / bs() * bs();
       const int64_t num_free = (int64_t)free_blocks.size();

@@ -47,7 +47,7 @@ class LLMEngine:
             num_blocks = max_live_seqs * ((self.max_seq_len + block_size - 1) // block_size)
         self.runner = ModelRunner(cfg, device, num_blocks, block_size, self.max_seq_len,
                                   min(max_num_seqs, max_live_seqs, 512), enforce_eager, seed,
-                                  gpu_memory_utilization or 0.9)
+                                  gpu_memory_utilization or 0.9, max_num_batched_tokens, max_num_seqs)
         num_blocks = self.runner.num_blocks
         self.scheduler = HostScheduler(num_blocks, block_size, max_num_seqs, max_num_batched_tokens,
                                        chunked_prefill_size, max_live_seqs, eos, self.max_seq_len)

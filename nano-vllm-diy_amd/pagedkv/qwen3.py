@@ -65,15 +65,24 @@ class Qwen3Weights:
 class Qwen3Model:
     """Forward over one step's tokens; K/V caches are (L, NB, BS, Hkv, D) per operand."""
 
-    def __init__(self, cfg: Qwen3Config, weights: Qwen3Weights, k_caches: torch.Tensor,
-                 v_caches: torch.Tensor, max_position: int):
+    def __init__(self, cfg: Qwen3Config, weights: Qwen3Weights, k_caches: torch.Tensor | None,
+                 v_caches: torch.Tensor | None, max_position: int):
+        """k_caches / v_caches None: no cache yet (the warmup pass before the cache is sized,
+        as the reference's Attention skips the store while k_cache is empty,
+        attention.py:87-88); bind_caches attaches them later."""
         self.cfg = cfg
         self.w = weights
-        self.k_caches = k_caches
-        self.v_caches = v_caches
+        self.bind_caches(k_caches, v_caches)
         dev = weights.embed.device
         self.cos_sin = ops.rope_cos_sin(max_position, cfg.head_dim, cfg.rope_theta, dev)
         self.scale = cfg.head_dim ** -0.5
+
+    def bind_caches(self, k_caches: torch.Tensor | None, v_caches: torch.Tensor | None) -> None:
+        """Per-layer K/V cache views, (L, NB, BS, Hkv, D) per operand (model_runner.py:161-165)."""
+        if (k_caches is None) != (v_caches is None):
+            raise ValueError("bind both caches or neither")
+        self.k_caches = k_caches
+        self.v_caches = v_caches
 
     def linear_workspace_bytes(self, max_rows: int) -> int:
         """Scratch the decode-step linear layers need for any batch of up to `max_rows`
@@ -113,7 +122,7 @@ class Qwen3Model:
             elif not small:
                 x, residual = ops.add_rmsnorm(h, L["input_norm"], eps, residual=residual)
             qkv = ops.linear(x, L["qkv"]) if small else F.linear(x, L["qkv"])
-            kc, vc = self.k_caches[li], self.v_caches[li]
+            kc, vc = (None, None) if self.k_caches is None else (self.k_caches[li], self.v_caches[li])
             if decode:
                 # one launch: q/k norm + RoPE, the K/V store and paged decode attention; no
                 # block is shared (no prefix cache), so every decode read streams

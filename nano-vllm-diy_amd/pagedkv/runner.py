@@ -69,27 +69,57 @@ def kv_cache_num_blocks(num_layers: int, block_size: int, num_kv_heads: int, hea
 class ModelRunner:
     def __init__(self, cfg: Qwen3Config, device: torch.device | str, num_blocks: int | None,
                  block_size: int = 256, max_seq_len: int = 8192, max_graph_bs: int = 128,
-                 enforce_eager: bool = False, seed: int = 5, gpu_memory_utilization: float = 0.9):
-        """num_blocks None: as many cache blocks as fit in gpu_memory_utilization of the
-        device once the weights are in place (kv_cache_num_blocks)."""
+                 enforce_eager: bool = False, seed: int = 5, gpu_memory_utilization: float = 0.9,
+                 max_num_batched_tokens: int = 16384, max_num_seqs: int = 512):
+        """As the reference's runner (model_runner.py:35-56): the weights, a warmup forward at
+        the largest step (warmup_model), then the KV cache -- num_blocks None: as many blocks
+        as fit in gpu_memory_utilization of the device beside the weights and the warmup's
+        activation peak (kv_cache_num_blocks) -- then the decode graphs."""
         self.cfg = cfg
         self.dev = torch.device(device)
         self.block_size = block_size
         self.max_seq_len = max_seq_len
         L, Hkv, D = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
         self.weights = Qwen3Weights(cfg, self.dev, seed)
+        self.model = Qwen3Model(cfg, self.weights, None, None, cfg.max_position_embeddings)
+        self.warmup_model(max_num_batched_tokens, max_seq_len, max_num_seqs)
+        stats = torch.cuda.memory_stats(self.dev)
+        # what the sizing keeps free for activations: the warmup's peak above the weights
+        self.activation_headroom = stats["allocated_bytes.all.peak"] - stats["allocated_bytes.all.current"]
         if num_blocks is None:
             num_blocks = kv_cache_num_blocks(L, block_size, Hkv, D, gpu_memory_utilization, device=self.dev)
         self.num_blocks = num_blocks
         self.kv_cache = torch.empty(2, L, num_blocks, block_size, Hkv, D, dtype=torch.bfloat16,
                                     device=self.dev)
-        self.model = Qwen3Model(cfg, self.weights, self.kv_cache[0], self.kv_cache[1],
-                                cfg.max_position_embeddings)
+        self.model.bind_caches(self.kv_cache[0], self.kv_cache[1])
         self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
         self.graph_bs: list[int] = []
         self.buckets: list[int] = []
         if not enforce_eager and max_graph_bs > 0:
             self._capture(max_graph_bs)
+
+    def warmup_model(self, max_num_batched_tokens: int, max_seq_len: int, max_num_seqs: int) -> None:
+        """The reference's warmup_model (model_runner.py:116-129): free the allocator's cache,
+        reset its peak, run one prefill of min(budget, max_seq_len)-token sequences of token 0
+        filling the token budget (no KV cache yet: dense attention over the fresh keys, no
+        store), and free the cache again, so the peak records a forward pass's activations
+        above the weights. It also loads every library kernel the prefill path uses before the
+        cache is sized."""
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(self.dev)
+        seq_len = min(max_num_batched_tokens, max_seq_len)
+        num_seqs = max(1, min(max_num_batched_tokens // seq_len, max_num_seqs))
+        n = seq_len * num_seqs
+        cu = torch.arange(0, n + 1, seq_len, dtype=torch.int32, device=self.dev)
+        ctx = Context(is_prefill=True, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=seq_len,
+                      max_seqlen_k=seq_len, slot_mapping=None, context_lens=None, block_tables=None)
+        ids = torch.zeros(n, dtype=torch.int64, device=self.dev)
+        pos = torch.arange(seq_len, dtype=torch.int64, device=self.dev).repeat(num_seqs)
+        hidden = self.model.forward(ids, pos, ctx)
+        self.model.greedy(hidden, ctx)
+        torch.cuda.synchronize(self.dev)
+        del hidden
+        torch.cuda.empty_cache()
 
     # ------------------------------------------------------------------ eager ----
     def _to_dev(self, t: torch.Tensor) -> torch.Tensor:

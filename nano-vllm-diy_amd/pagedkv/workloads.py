@@ -30,6 +30,11 @@ from .context import Context
 
 HQ, HKV, HEAD_DIM, BLOCK_SIZE = 16, 8, 128, 256   # Qwen3-0.6B attention geometry
 ROW_BYTES = HKV * HEAD_DIM * 2                     # one token row of K (or V), bytes
+# One GPU's share of the heads under the reference's tensor parallelism, which splits the
+# query heads and the KV cache by kv head (src/models/qwen3.py:30-36,
+# src/engine/model_runner.py:153; tp defaults to 2 and may go up to 8,
+# src/config/runner_config.py:12,40): (Hq / tp, Hkv / tp).
+TP_HEADS = {1: (16, 8), 2: (8, 4), 4: (4, 2), 8: (2, 1)}
 
 WORKLOADS = ("cfg1_store", "cfg1_decode", "cfg2", "cfg3", "cfg4", "prefill_steady")
 
@@ -54,6 +59,19 @@ class Workload:
     attend: bool = True             # False: store-only workload
     unique_blocks: int = 0          # distinct physical blocks read by the attention
     meta: dict = field(default_factory=dict)
+
+    @property
+    def num_heads(self) -> int:
+        return int(self.q.shape[1])
+
+    @property
+    def num_kv_heads(self) -> int:
+        return int(self.k_cache.shape[2])
+
+    @property
+    def row_bytes(self) -> int:
+        """One token row of K (or V) in the cache, bytes: Hkv * D * 2."""
+        return self.num_kv_heads * HEAD_DIM * 2
 
     @property
     def ctx(self) -> Context:
@@ -82,14 +100,25 @@ class Workload:
     def store_bytes(self) -> int:
         """Read K and V rows, write K and V rows, read the slot: 4 N R + 4 N."""
         n = int(self.slot_mapping.numel())
-        return 4 * n * ROW_BYTES + 4 * n
+        return 4 * n * self.row_bytes + 4 * n
 
     def decode_kv_bytes(self) -> int:
         """K and V bytes the one-row sequences need: sum Lk * 2R."""
-        return sum(lk * 2 * ROW_BYTES for lq, lk in zip(self.q_lens, self.k_lens) if lq == 1 and lk > 0)
+        return sum(lk * 2 * self.row_bytes for lq, lk in zip(self.q_lens, self.k_lens) if lq == 1 and lk > 0)
 
     def decode_unique_kv_bytes(self) -> int:
-        return self.unique_blocks * BLOCK_SIZE * 2 * ROW_BYTES if self.unique_blocks else self.decode_kv_bytes()
+        """Distinct K and V bytes the one-row sequences need. With shared prefix blocks
+        (meta["shared_prefix"] keys, read by every sequence): (prefix + sum of the
+        suffixes) * 2R, the keys themselves, not the whole blocks that hold them."""
+        if "shared_prefix" in self.meta:
+            p = self.meta["shared_prefix"]
+            keys = p + sum(lk - p for lq, lk in zip(self.q_lens, self.k_lens) if lq == 1 and lk > 0)
+            return keys * 2 * self.row_bytes
+        return self.decode_kv_bytes()
+
+    def decode_unique_block_bytes(self) -> int:
+        """Bytes of the distinct cache blocks the one-row sequences read (whole blocks)."""
+        return self.unique_blocks * BLOCK_SIZE * 2 * self.row_bytes if self.unique_blocks else self.decode_kv_bytes()
 
     def prefill_flops(self) -> int:
         """sum 4 Hq D (Lq P + Lq (Lq + 1) / 2) over sequences with Lq > 1 (causal)."""
@@ -97,7 +126,7 @@ class Workload:
         for lq, lk in zip(self.q_lens, self.k_lens):
             if lq > 1:
                 p = lk - lq
-                tot += 4 * HQ * HEAD_DIM * (lq * p + lq * (lq + 1) // 2)
+                tot += 4 * self.num_heads * HEAD_DIM * (lq * p + lq * (lq + 1) // 2)
         return tot
 
     def to(self, device) -> "Workload":
@@ -108,7 +137,7 @@ class Workload:
         if base is not None:
             qkv = base.to(device)
             meta["qkv"] = qkv
-            v = _v_view(qkv, self.v.shape[0])
+            v = _v_view(qkv, self.v.shape[0], self.num_heads, self.num_kv_heads)
         else:
             v = mv(self.v)
         return Workload(self.name, mv(self.q), mv(self.k), v, mv(self.k_cache), mv(self.v_cache),
@@ -118,8 +147,8 @@ class Workload:
                         self.unique_blocks, meta)
 
 
-def _v_view(qkv: torch.Tensor, n: int) -> torch.Tensor:
-    return qkv[:, (HQ + HKV) * HEAD_DIM:].view(n, HKV, HEAD_DIM)
+def _v_view(qkv: torch.Tensor, n: int, hq: int = HQ, hkv: int = HKV) -> torch.Tensor:
+    return qkv[:, (hq + hkv) * HEAD_DIM:].view(n, hkv, HEAD_DIM)
 
 
 def slots_for(block_table: list[int], start: int, end: int, block_size: int = BLOCK_SIZE) -> list[int]:
@@ -134,9 +163,11 @@ def _randn(shape, gen: torch.Generator, device) -> torch.Tensor:
 
 
 def _assemble(name: str, seqs: list[tuple[int, int, list[int]]], num_blocks: int, seed: int,
-              device, attend: bool = True, unique_blocks: int = 0, meta: dict | None = None) -> Workload:
+              device, attend: bool = True, unique_blocks: int = 0, meta: dict | None = None,
+              heads: tuple[int, int] = (HQ, HKV)) -> Workload:
     """seqs: (Lq, Lk, block_table) per sequence in batch order; new tokens are the
-    last Lq positions of each sequence."""
+    last Lq positions of each sequence. heads = (Hq, Hkv)."""
+    hq, hkv = heads
     dev = torch.device(device)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -147,12 +178,12 @@ def _assemble(name: str, seqs: list[tuple[int, int, list[int]]], num_blocks: int
     for lq, lk, bt in seqs:
         slots += slots_for(bt, lk - lq, lk)
     width = max((len(s[2]) for s in seqs), default=0)
-    k_cache = _randn((num_blocks, BLOCK_SIZE, HKV, HEAD_DIM), gen, dev)
-    v_cache = _randn((num_blocks, BLOCK_SIZE, HKV, HEAD_DIM), gen, dev)
-    qkv = _randn((n, (HQ + 2 * HKV) * HEAD_DIM), gen, dev)
-    q = qkv[:, :HQ * HEAD_DIM].reshape(n, HQ, HEAD_DIM).clone()
-    k = qkv[:, HQ * HEAD_DIM:(HQ + HKV) * HEAD_DIM].reshape(n, HKV, HEAD_DIM).clone()
-    v = _v_view(qkv, n)
+    k_cache = _randn((num_blocks, BLOCK_SIZE, hkv, HEAD_DIM), gen, dev)
+    v_cache = _randn((num_blocks, BLOCK_SIZE, hkv, HEAD_DIM), gen, dev)
+    qkv = _randn((n, (hq + 2 * hkv) * HEAD_DIM), gen, dev)
+    q = qkv[:, :hq * HEAD_DIM].reshape(n, hq, HEAD_DIM).clone()
+    k = qkv[:, hq * HEAD_DIM:(hq + hkv) * HEAD_DIM].reshape(n, hkv, HEAD_DIM).clone()
+    v = _v_view(qkv, n, hq, hkv)
     bts = torch.full((len(seqs), width), -1, dtype=torch.int32)
     for i, (_, _, bt) in enumerate(seqs):
         bts[i, :len(bt)] = torch.tensor(bt, dtype=torch.int32)
@@ -192,10 +223,16 @@ def _uniform(gen: torch.Generator, lo: int, hi: int, n: int) -> list[int]:
 
 
 def make_workload(name: str, device="cpu", seed: int | None = None,
-                  num_seqs: int | None = None) -> Workload:
-    """Build one of WORKLOADS. num_seqs shrinks the batch (tests); None = full size."""
+                  num_seqs: int | None = None, heads: tuple[int, int] = (HQ, HKV)) -> Workload:
+    """Build one of WORKLOADS. num_seqs shrinks the batch (tests); None = full size.
+    heads = (Hq, Hkv): the whole model's (16, 8) or one tensor-parallel rank's share
+    (TP_HEADS); lengths and block tables do not depend on it."""
     if name not in WORKLOADS:
         raise ValueError(f"unknown workload {name!r}; choose from {WORKLOADS}")
+    hq, hkv = heads
+    if hq <= 0 or hkv <= 0 or hq % hkv:
+        raise ValueError(f"heads {heads}: Hq must be a positive multiple of Hkv")
+    kw = {"heads": (hq, hkv)}
     cfg_seed = {"cfg1_store": 1, "cfg1_decode": 1, "cfg2": 2, "cfg3": 3, "cfg4": 4, "prefill_steady": 5}[name]
     seed = cfg_seed if seed is None else seed
     host = torch.Generator()
@@ -212,9 +249,9 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
         pool = torch.randperm(nb, generator=host).tolist()
         if name == "cfg1_store":
             bt = store_pool[:math.ceil(n_store / BLOCK_SIZE)]
-            return _assemble(name, [(n_store, n_store, bt)], nb, seed * 1000 + 11, device, attend=False)
+            return _assemble(name, [(n_store, n_store, bt)], nb, seed * 1000 + 11, device, attend=False, **kw)
         tables = _pop_tables(lks, pool)
-        return _assemble(name, [(1, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 12, device)
+        return _assemble(name, [(1, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 12, device, **kw)
 
     if name == "cfg2":
         # decode at serving scale: S = 256, Lk ~ U[1024, 8192], pool = exactly the blocks needed
@@ -224,7 +261,7 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
         pool = torch.randperm(nb, generator=host).tolist()
         tables = _pop_tables(lks, pool)
         return _assemble(name, [(1, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 2, device,
-                         unique_blocks=nb)
+                         unique_blocks=nb, **kw)
 
     if name == "cfg3":
         # mixed batch: 128 decodes (Lk ~ U[512, 4096]) first, then 8 prefill chunks of
@@ -241,7 +278,7 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
         seqs = [(1, lk, bt) for lk, bt in zip(dec_lks, tables[:n_dec])]
         seqs += [(chunk, lk, bt) for lk, bt in zip(lks[n_dec:], tables[n_dec:])]
         return _assemble(name, seqs, nb, seed * 1000 + 3, device, unique_blocks=0,
-                         meta={"prefixes": prefixes})
+                         meta={"prefixes": prefixes}, **kw)
 
     if name == "prefill_steady":
         # chunked prefill large enough to keep every CU busy: 16 chunks of 1024 tokens, each
@@ -252,7 +289,7 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
         nb = sum(math.ceil(lk / BLOCK_SIZE) for lk in lks)
         pool = torch.randperm(nb, generator=host).tolist()
         tables = _pop_tables(lks, pool)
-        return _assemble(name, [(chunk, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 5, device)
+        return _assemble(name, [(chunk, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 5, device, **kw)
 
     # cfg4: 64 sequences share one 2048-token prefix (8 physical blocks, refcount 64);
     # private suffixes of U[256, 1024] tokens.
@@ -267,7 +304,7 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
     tables = [shared + t for t in _pop_tables(suffixes, private)]
     seqs = [(1, prefix + x, bt) for x, bt in zip(suffixes, tables)]
     return _assemble(name, seqs, nb, seed * 1000 + 4, device, unique_blocks=nb,
-                     meta={"shared_blocks": shared})
+                     meta={"shared_blocks": shared, "shared_prefix": prefix}, **kw)
 
 
 def serving_requests(seed: int = 5, num_requests: int = 256, vocab_size: int = 151936,

@@ -122,7 +122,7 @@ def test_flat_graph_padding_and_truncation(gpu):
     _assert_within_merge_rounding(base, pad)
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (16, 2)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (16, 2), (8, 4), (2, 1)])
 def test_flat_fused_decode_bit_identical(gpu, hq, hkv):
     """pk_qkv_decode_attention against pk_qk_norm_rope_store + pk_varlen_attention_ex on a
     flat-grid batch with graph padding: output and caches bit for bit."""

@@ -70,7 +70,8 @@ def _assert_same(a, b, S):
     assert torch.equal(vca.view(torch.int16), vcb.view(torch.int16)), "V cache differs"
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4), (16, 2)])
+# (8, 4), (4, 2), (2, 1): one tensor-parallel rank's share at tp 2, 4, 8 (qwen3.py:30-36)
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4), (16, 2), (8, 4), (4, 2), (2, 1)])
 @pytest.mark.parametrize("lens,pad", [([1, 5, 255, 256, 257, 3000], 0), ([700, 12, 4096, 1], 3)])
 def test_fused_decode_bit_identical_to_producer_then_attention(gpu, hq, hkv, lens, pad):
     cs = pagedkv.rope_cos_sin(MAX_POS, D, 1000000.0, gpu)

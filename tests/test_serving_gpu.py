@@ -5,12 +5,14 @@ size 256, 16384-token budget -- the workload bench.py times.
 
 Checks:
   * every request gets exactly its max_tokens outputs and every block returns to the pool;
-  * three whole sequences, teacher-forced through the 28-layer CPU model oracle
+  * four whole sequences, teacher-forced through the 28-layer CPU model oracle
     (oracle/qwen3.py): a prompt long enough to be prefilled in two chunks, a request whose
-    1018 outputs span most of the run's decode steps, and the shortest request. Every
+    1018 outputs span most of the run's decode steps, the shortest request, and the request
+    with the longest context (974 prompt + 985 output tokens, whose last decode steps read
+    up to 1958 cached keys, in the largest graph bucket and cut into the most pieces). Every
     generated token's logit must lie within LOGIT_TOL of the oracle's maximum at its position,
     and >= 90% of the tokens must be the oracle's argmax;
-  * graph vs eager: the same three requests on an eager engine (no HIP graphs, other batch
+  * graph vs eager: the same four requests on an eager engine (no HIP graphs, other batch
     composition) are checked the same way, teacher-forced through the oracle. With random
     weights the logits of a step lie close together, so the two runs part at the first
     near-tie that bf16 rounding decides differently (both tokens within LOGIT_TOL of the
@@ -34,7 +36,9 @@ def _pick(prompts, max_tokens):
     chunked = max(short, key=lambda i: len(prompts[i]))
     long_out = max(short, key=lambda i: max_tokens[i])
     shortest = min(range(len(prompts)), key=lambda i: total[i])
-    return [chunked, long_out, shortest]
+    # the longest context of the run (1959 tokens: decode steps in the 2048-key graph bucket)
+    longest = max(range(len(prompts)), key=lambda i: total[i])
+    return [chunked, long_out, shortest, longest]
 
 
 def test_serving_workload_full_size(gpu):
@@ -54,6 +58,7 @@ def test_serving_workload_full_size(gpu):
 
     sel = _pick(prompts, max_tokens)
     assert len(prompts[sel[0]]) > 512                                  # prefilled in two chunks
+    assert len(prompts[sel[3]]) + max_tokens[sel[3]] >= 1900
     print(f"[serving] eager engine on requests {sel}", flush=True)
     eager = E.LLMEngine(cfg, device=gpu, num_blocks=64, block_size=256, max_num_batched_tokens=16384, seed=5,
                         enforce_eager=True)

@@ -35,25 +35,37 @@ def _with_workspace(w, hint):
     return out
 
 
-def _no_alloc(w, hint):
+def _no_alloc(w, hint, out):
     lib = _lib.lib()
-    out = torch.zeros_like(w.q)
     stream = torch.cuda.current_stream().cuda_stream
     _lib.check(lib.pk_varlen_attention_noalloc(*_args(w, out), hint, stream), "pk_varlen_attention_noalloc")
     return out
 
 
 def test_no_alloc_matches_workspace_entry_point(gpu):
+    """Every workload, its reference output and its output buffers are made first; after one
+    call (the first on the device looks the scratch's address up) the device's free memory
+    must not move while the remaining calls run: the entry point allocates nothing."""
     # largest first: every later call reads scratch bytes an earlier, bigger call wrote
     cases = [("cfg3", None, 0), ("cfg2", 64, 0), ("cfg4", 16, 2048), ("cfg1_decode", None, 0), ("cfg2", 5, -1)]
+    runs = []
     for name, num_seqs, hint in cases:
-        print(f"[no_alloc] {name} num_seqs={num_seqs} hint={hint}", flush=True)
         w = make_workload(name, gpu, num_seqs=num_seqs)
         want = _with_workspace(w, hint)
-        got = _no_alloc(w, hint)
-        torch.cuda.synchronize()
-        assert bits_equal(got, want), f"{name} ({num_seqs} sequences)"
-        again = _no_alloc(w, hint)          # the same call again, on the scratch it left
-        torch.cuda.synchronize()
-        assert bits_equal(again, want), f"{name} ({num_seqs} sequences), second call"
-
+        runs.append((name, num_seqs, hint, w, want, torch.zeros_like(w.q), torch.zeros_like(w.q)))
+    torch.cuda.synchronize()
+    name, num_seqs, hint, w, _, first, _ = runs[0]
+    print(f"[no_alloc] first call: {name} num_seqs={num_seqs} hint={hint}", flush=True)
+    _no_alloc(w, hint, first)
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info(gpu)[0]
+    for name, num_seqs, hint, w, want, out1, out2 in runs:
+        print(f"[no_alloc] {name} num_seqs={num_seqs} hint={hint}", flush=True)
+        _no_alloc(w, hint, out1)
+        _no_alloc(w, hint, out2)            # the same call again, on the scratch it left
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(gpu)[0] == free_before, "device memory changed during the calls"
+    assert bits_equal(first, runs[0][4]), "first call"
+    for name, num_seqs, hint, w, want, out1, out2 in runs:
+        assert bits_equal(out1, want), f"{name} ({num_seqs} sequences)"
+        assert bits_equal(out2, want), f"{name} ({num_seqs} sequences), second call"
