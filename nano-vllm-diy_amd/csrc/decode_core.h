@@ -11,8 +11,16 @@ namespace {
 #ifndef PK_DECODE_STEP_G2
 #define PK_DECODE_STEP_G2 8     // keys per pipeline step for GQA groups <= 2
 #endif
-// Keys per pipeline step of the decode units built for a GQA group.
+// Keys per pipeline step and DPP row of the decode units built for a GQA group.
 constexpr int decode_step_keys(int group) { return group <= 2 ? PK_DECODE_STEP_G2 : 4; }
+// DPP rows per kv head (key rows): a wavefront's four 16-lane rows hold four kv heads, or,
+// with fewer kv heads than that (one tensor-parallel rank's share: 2 or 1), 4 / Hkv rows per
+// head that take interleaved keys, so that no row re-reads another's head.
+constexpr int decode_key_rows(int num_kv_heads) { return num_kv_heads == 1 ? 4 : num_kv_heads == 2 ? 2 : 1; }
+// Keys a wavefront consumes per pipeline step: the flat grid's step.
+inline int decode_flat_step(int group, int num_kv_heads) {
+  return decode_step_keys(group) * decode_key_rows(num_kv_heads);
+}
 
 constexpr int kStoreThrough = 16;  // buffer cache policy bit sc1: write through L2
 // Partial footprint (launch bound: sequences x splits x heads x D x 4 bytes) above which the
@@ -83,13 +91,19 @@ __device__ __forceinline__ int scalar_block_id(const int32_t* row, int j) {
   return v;
 }
 
-template <int U, bool PAGED, bool STREAM, bool FUSED>
-__device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_bytes, int b, int k0, int t,
+// R key rows per kv head (decode_key_rows): DPP row j of a head takes keys t + u R + j of
+// the step's U R keys, so one load instruction reads R consecutive token rows. Its lane
+// offsets lane_k / lane_v include row j's key (j row strides), and the loads are bounded
+// by the buffer's range instead of clamped (a row's key past t_end reads zeros, finite,
+// masked to p = 0 by consume): the row offset is per lane, which a scalar offset cannot
+// carry.
+template <int U, int R, bool PAGED, bool STREAM, bool FUSED>
+__device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_k, uint32_t lane_v, int b, int k0, int t,
                                             int t_end, u32x4 (&kr)[U], u32x4 (&vr)[U]) {
   const uint16_t* kp;
   const uint16_t* vp;
   if constexpr (PAGED) {
-    // [t, t + U) lies inside one cache block: U divides block_size and split_tokens.
+    // [t, t + U R) lies inside one cache block: U R divides block_size and split_tokens.
     const int blk = FUSED ? scalar_block_id(a.block_table + (int64_t)b * a.bt_stride, t / a.block_size)
                           : a.block_table[(int64_t)b * a.bt_stride + t / a.block_size];
     const int off = t % a.block_size;
@@ -99,16 +113,26 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_byt
     kp = a.k + (int64_t)(k0 + t) * a.k_row_stride;
     vp = a.v + (int64_t)(k0 + t) * a.v_row_stride;
   }
-  // row strides are < 2^22 elements (checked on the host), so U rows span < 2^27 bytes
+  // row strides are < 2^22 elements (checked on the host), so U R rows span < 2^29 bytes
   const uint32_t k_row_bytes = (uint32_t)a.k_row_stride * 2u;
   const uint32_t v_row_bytes = (uint32_t)a.v_row_stride * 2u;
-  const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, (uint32_t)U * k_row_bytes);
-  const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, (uint32_t)U * v_row_bytes);
-  const int last = t_end - 1 - t;
+  if constexpr (R == 1) {
+    const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, (uint32_t)U * k_row_bytes);
+    const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, (uint32_t)U * v_row_bytes);
+    const int last = t_end - 1 - t;
 #pragma unroll
-  for (int u = 0; u < U; ++u) kr[u] = load16<STREAM>(kr_rs, lane_bytes, __umul24((uint32_t)min(u, last), k_row_bytes));
+    for (int u = 0; u < U; ++u) kr[u] = load16<STREAM>(kr_rs, lane_k, __umul24((uint32_t)min(u, last), k_row_bytes));
 #pragma unroll
-  for (int u = 0; u < U; ++u) vr[u] = load16<STREAM>(vr_rs, lane_bytes, __umul24((uint32_t)min(u, last), v_row_bytes));
+    for (int u = 0; u < U; ++u) vr[u] = load16<STREAM>(vr_rs, lane_v, __umul24((uint32_t)min(u, last), v_row_bytes));
+  } else {
+    const uint32_t rows = (uint32_t)min(U * R, t_end - t);  // keys of the step that exist
+    const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, rows * k_row_bytes);
+    const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, rows * v_row_bytes);
+#pragma unroll
+    for (int u = 0; u < U; ++u) kr[u] = load16<STREAM>(kr_rs, lane_k + (uint32_t)(u * R) * k_row_bytes, 0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) vr[u] = load16<STREAM>(vr_rs, lane_v + (uint32_t)(u * R) * v_row_bytes, 0);
+  }
 }
 
 // Keys [t_begin, t_end) of one split through a two-stage software pipeline: the loads of
@@ -117,13 +141,14 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_byt
 // and the wait counts stay exact. The scheduling barriers keep each step's loads together
 // ahead of its math: otherwise the scheduler sinks every load next to its first use to
 // save registers, which serialises their latency.
-template <int G, int U, bool PAGED, bool STREAM, bool FUSED, class Pre>
-__device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
-                                             int k0, int t_begin, int t_end, Pre&& pre);
+template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, class Pre>
+__device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_k, uint32_t lane_v,
+                                             int j, int b, int k0, int t_begin, int t_end, Pre&& pre);
 
-// Fold keys [t, t + U) (already loaded) into the running softmax state.
-template <int G, int U>
-__device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int t_end, const u32x4 (&kr)[U],
+// Fold this row's keys of the step at t (already loaded: key t + u R + j for load u) into the
+// running softmax state.
+template <int G, int U, int R>
+__device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int t_end, int j, const u32x4 (&kr)[U],
                                         const u32x4 (&vr)[U]) {
   // unscaled scores: 4 dot2 per (key, head) over this lane's 8 elements, then the
   // 16-lane DPP sum gives every lane of the row the full q.k of its key.
@@ -138,7 +163,7 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
       d0 = dot2(st.qp[i][3], kr[u].w, d0);
       s[u][i] = row16_sum(d0);
     }
-    if (t + u >= t_end) {
+    if (t + u * R + (R > 1 ? j : 0) >= t_end) {  // uniform over the wavefront when R == 1
 #pragma unroll
       for (int i = 0; i < G; ++i) s[u][i] = -INFINITY;
     }
@@ -152,10 +177,12 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
     float mx = s[0][i];
 #pragma unroll
     for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][i]);
-    const float m_new = fmaxf(st.m[i], mx);  // finite: the step holds >= 1 valid key
-    const float alpha = exp2_fast((st.m[i] - m_new) * c2);
+    // R == 1: finite, the step holds >= 1 valid key. R > 1: a row may not have had a key
+    // yet (-inf); its l and numerator are 0, and alpha and the exponents must stay finite.
+    const float m_new = fmaxf(st.m[i], mx);
+    const float alpha = (R > 1 && st.m[i] == -INFINITY) ? 0.f : exp2_fast((st.m[i] - m_new) * c2);
     st.m[i] = m_new;
-    const float ms = m_new * c2;
+    const float ms = (R > 1 && m_new == -INFINITY) ? 0.f : m_new * c2;
     st.l[i] *= alpha;
 #pragma unroll
     for (int e = 0; e < 8; ++e) st.acc[i][e] *= alpha;
@@ -187,23 +214,48 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
   }
 }
 
-template <int G, int U, bool PAGED, bool STREAM, bool FUSED, class Pre>
-__device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_bytes, int b,
-                                             int k0, int t_begin, int t_end, Pre&& pre) {
+template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, class Pre>
+__device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_k, uint32_t lane_v,
+                                             int j, int b, int k0, int t_begin, int t_end, Pre&& pre) {
+  constexpr int S = U * R;  // keys per step
   const float c2 = a.scale_log2;
   u32x4 kA[U], vA[U], kB[U], vB[U];
-  issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t_begin, t_end, kA, vA);
+  issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t_begin, t_end, kA, vA);
   pre();  // q (loaded or computed) while the first K/V loads are in flight
-  for (int t = t_begin; t < t_end; t += 2 * U) {
-    const int t1 = t + U;
-    issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
+  for (int t = t_begin; t < t_end; t += 2 * S) {
+    const int t1 = t + S;
+    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
     __builtin_amdgcn_sched_barrier(0);
-    consume<G, U>(st, c2, t, t_end, kA, vA);
+    consume<G, U, R>(st, c2, t, t_end, j, kA, vA);
     if (t1 >= t_end) break;
-    const int t2 = t1 + U;
-    issue_loads<U, PAGED, STREAM, FUSED>(a, lane_bytes, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
+    const int t2 = t1 + S;
+    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
     __builtin_amdgcn_sched_barrier(0);
-    consume<G, U>(st, c2, t1, t_end, kB, vB);
+    consume<G, U, R>(st, c2, t1, t_end, j, kB, vB);
+  }
+}
+
+// R > 1: merge the softmax states of the R rows that hold one kv head's interleaved keys
+// (rows j = row / (4 / R), lanes 16 (4 / R) apart), so that every row of the head ends with
+// the state over all of the unit's keys. A row that saw no key (m = -inf) adds nothing.
+template <int G, int R>
+__device__ __forceinline__ void merge_key_rows(DecodeState<G>& st, float c2) {
+  if constexpr (R > 1) {
+#pragma unroll
+    for (int sh = 64 / R; sh < kWave; sh *= 2) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const float mo = __shfl_xor(st.m[i], sh);
+        const float lo = __shfl_xor(st.l[i], sh);
+        const float m_new = fmaxf(st.m[i], mo);
+        const float wa = st.m[i] == -INFINITY ? 0.f : exp2_fast((st.m[i] - m_new) * c2);
+        const float wb = mo == -INFINITY ? 0.f : exp2_fast((mo - m_new) * c2);
+        st.l[i] = st.l[i] * wa + lo * wb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.acc[i][e] = st.acc[i][e] * wa + __shfl_xor(st.acc[i][e], sh) * wb;
+        st.m[i] = m_new;
+      }
+    }
   }
 }
 
@@ -278,18 +330,27 @@ __device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>
 // flat mode, Lk keys in all) for the kv heads of this wavefront. direct: the unit holds every
 // key of the sequence, so it normalises and writes the output row itself; otherwise it
 // leaves its (max, sum, numerator) partial at partial unit unit0 (x num_heads) for the combine.
-template <int G, int U, bool PAGED, bool FUSED>
+// R key rows per kv head: DPP row r holds kv head g_first + r mod (4 / R) and keys
+// t + u R + r / (4 / R) of every step; the rows of a head merge their states at the end.
+template <int G, int U, int R, bool PAGED, bool FUSED>
 __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_first, int b, int q0, int k0, int Lk,
                                             int t_begin, int t_end, bool direct, int64_t unit0) {
   static_assert(U % 2 == 0, "P.V pairs keys");
+  static_assert(R == 1 || R == 2 || R == 4, "key rows per kv head");
   constexpr int D = kHeadDim;
+  constexpr int NH = 4 / R;                               // kv heads per wavefront
   const int c = lane & 15;
-  const int g_lane = g_first + (lane >> 4);               // this DPP row's kv head
+  const int row = lane >> 4;
+  const int j = row / NH;                                 // this row's keys: t + u R + j
+  const int g_lane = g_first + row % NH;                  // this DPP row's kv head
   const bool row_live = g_lane < a.num_kv_heads;
+  const bool writer = row_live && j == 0;                 // stores the head's results
   const int g = row_live ? g_lane : a.num_kv_heads - 1;   // idle rows read a valid head
   const int H = a.num_heads;
   const float c2 = a.scale_log2;
   const uint32_t lane_bytes = (uint32_t)(g * D + c * 8) * 2u;
+  const uint32_t lane_k = lane_bytes + (uint32_t)j * (uint32_t)a.k_row_stride * 2u;
+  const uint32_t lane_v = lane_bytes + (uint32_t)j * (uint32_t)a.v_row_stride * 2u;
 
   // q stays in bf16 pairs: q.k runs on v_dot2_f32_bf16 and the scale is applied to the
   // fp32 dot product (scores are kept unscaled; c2 enters the exponent). q is loaded (or,
@@ -306,7 +367,7 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
   }
   const auto load_q = [&]() {
     if constexpr (FUSED) {
-      fused_producer<G>(a, st, q0, g, c, row_live, false);
+      fused_producer<G>(a, st, q0, g, c, writer, false);
     } else {
 #pragma unroll
       for (int i = 0; i < G; ++i) {
@@ -326,18 +387,19 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
   // once per step and only displaces useful lines. Decided per split (by its first key).
   const bool stream = a.stream_from >= 0 && t_begin >= a.stream_from;
   if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
-    fused_producer<G>(a, st, q0, g, c, row_live, true);
+    fused_producer<G>(a, st, q0, g, c, writer, true);
     if (stream)
-      decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, nothing);
+      decode_range<G, U, R, PAGED, true, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, nothing);
     else
-      decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, nothing);
+      decode_range<G, U, R, PAGED, false, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, nothing);
   } else if (stream) {
-    decode_range<G, U, PAGED, true, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
+    decode_range<G, U, R, PAGED, true, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, load_q);
   } else {
-    decode_range<G, U, PAGED, false, FUSED>(st, a, lane_bytes, b, k0, t_begin, t_end, load_q);
+    decode_range<G, U, R, PAGED, false, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, load_q);
   }
+  merge_key_rows<G, R>(st, c2);
 
-  if (!row_live) return;
+  if (!writer) return;
   // Partials of this unit: H heads x (D outputs in bf16, (max, sum)), contiguous, written
   // through L2 or left in it by the launch's choice (kStoreThroughBytes). A unit holds >= 1
   // key, so l >= 1 (its largest score contributes exp2(0)).

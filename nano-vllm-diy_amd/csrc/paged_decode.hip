@@ -69,12 +69,12 @@ constexpr int kDecodeMaxWaves = PK_DECODE_WAVES;
 
 // Split mode: grid (splits x sequences, kv-head groups); a work-group takes split `split` of
 // one sequence (split_tokens keys after the shared prefix, if any).
-template <int G, int U, bool PAGED, bool FUSED>
+template <int G, int U, int R, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(const AttnArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
   // The launch divides the kv heads evenly over the waves: every wave has >= 1 live row.
-  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;   // first kv head of the wave
+  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * (4 / R);  // first kv head of the wave
   // Work-groups are dispatched round-robin over the 8 XCDs in linear id order. Split-major
   // order with the sequence rotated by the split index sends consecutive splits of one
   // sequence to consecutive XCDs, so every XCD gets about 1/8 of each sequence whatever the
@@ -96,8 +96,8 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
   // partials of the sequence: its prefix chunks, then its splits
   const int nsplit = (Pb + a.prefix_chunk - 1) / a.prefix_chunk + (Lk - Pb + a.split_tokens - 1) / a.split_tokens;
   const int slot = a.prefix_slots + split;
-  decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, nsplit == 1,
-                                  ((int64_t)b * a.max_splits + slot) * a.num_heads);
+  decode_unit<G, U, R, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, nsplit == 1,
+                                     ((int64_t)b * a.max_splits + slot) * a.num_heads);
 }
 
 // Flat mode: the decode keys of the batch -- per decode sequence b the c_b keys after its
@@ -119,11 +119,12 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
 // wavefront prefix sum and finds the work-group's sequence with one ballot per slot.
 constexpr int kFlatSlots = 8;
 
-template <int G, int U, bool PAGED, bool FUSED>
+template <int G, int U, int R, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(const AttnArgs a) {
+  constexpr int ST = U * R;  // keys per pipeline step: the line's step
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * 4;
+  const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * (4 / R);
   const int n = a.num_seqs;
   // lane l, slot s: sequence e = l + 64 s
   int kb[kFlatSlots], qb[kFlatSlots], lk[kFlatSlots], cnt[kFlatSlots], pos[kFlatSlots];
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(con
     }
   }
   const int per = (T + a.flat_groups - 1) / a.flat_groups;
-  const int chunk = max(a.flat_min_chunk, (per + U - 1) / U * U);
+  const int chunk = max(a.flat_min_chunk, (per + ST - 1) / ST * ST);
   const int u = blockIdx.x;
   // the decode sequence with b + w0(b) <= u <= b + w1(b), if any
   int b = -1, q0 = 0, k0 = 0, Lk = 0, p0 = 0, cb = 0;
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(con
     if (64 * s < n) {
       const int e = lane + 64 * s;
       const int w0 = pos[s] / chunk;
-      const int w1 = (pos[s] + (cnt[s] - 1) / U * U) / chunk;
+      const int w1 = (pos[s] + (cnt[s] - 1) / ST * ST) / chunk;
       const uint64_t m = __builtin_amdgcn_ballot_w64(cnt[s] > 0 && e + w0 <= u && u <= e + w1);
       if (m) {
         const int j = __builtin_ctzll(m);
@@ -183,12 +184,12 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(con
   }
   const int Pb = Lk - cb;                                // keys of the shared prefix
   const int F0 = (u - b) * chunk, F1 = F0 + chunk;       // this run, on the line
-  const int t_begin = Pb + (F0 > p0 ? (F0 - p0 + U - 1) / U * U : 0);
-  const int t_end = min(Lk, Pb + (F1 - p0 + U - 1) / U * U);
+  const int t_begin = Pb + (F0 > p0 ? (F0 - p0 + ST - 1) / ST * ST : 0);
+  const int t_end = min(Lk, Pb + (F1 - p0 + ST - 1) / ST * ST);
   // the sequence's first and last steps in one run and no prefix partial: this piece is all of it
-  const bool direct = Pb == 0 && p0 / chunk == (p0 + (cb - 1) / U * U) / chunk;
-  decode_unit<G, U, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
-                                  ((int64_t)a.flat_unit0 + u) * a.num_heads);
+  const bool direct = Pb == 0 && p0 / chunk == (p0 + (cb - 1) / ST * ST) / chunk;
+  decode_unit<G, U, R, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
+                                     ((int64_t)a.flat_unit0 + u) * a.num_heads);
 }
 
 // EAGER > 0 (small split-grid batches without a shared prefix, max_splits <= EAGER): the
@@ -210,12 +211,13 @@ bool eager_combine(const AttnArgs& a) {
          (int64_t)a.grid_splits * a.num_seqs <= 1024;
 }
 
-template <int G, int U>
+template <int G, int U, int R>
 hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   const bool flat = a.flat_groups > 0;
   const int64_t units = flat ? (int64_t)a.num_seqs + a.flat_groups : (int64_t)a.num_seqs * a.max_splits;  // decode kernel's
   a.store_through = units * a.num_heads * kHeadDim * 4 > kStoreThroughBytes;
-  const int quads = (a.num_kv_heads + 3) / 4;   // wavefronts needed for all kv heads
+  constexpr int NH = 4 / R;                     // kv heads per wavefront
+  const int quads = (a.num_kv_heads + NH - 1) / NH;  // wavefronts needed for all kv heads
   int waves = quads < kDecodeMaxWaves ? quads : kDecodeMaxWaves;
   while (quads % waves != 0) --waves;            // no idle wavefront in any work-group
   const int zgroups = quads / waves;
@@ -224,22 +226,33 @@ hipError_t launch_decode_g(AttnArgs a, bool paged, hipStream_t stream) {
   if (flat) {
     const dim3 grid((unsigned)(a.flat_groups + a.num_seqs + 1), (unsigned)zgroups);  // + the recorder
     if (fused)
-      hipLaunchKernelGGL((decode_flat_kernel<G, U, true, true>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((decode_flat_kernel<G, U, R, true, true>), grid, block, 0, stream, a);
     else if (paged)
-      hipLaunchKernelGGL((decode_flat_kernel<G, U, true, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((decode_flat_kernel<G, U, R, true, false>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL((decode_flat_kernel<G, U, false, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((decode_flat_kernel<G, U, R, false, false>), grid, block, 0, stream, a);
     return hipGetLastError();
   }
   if (a.grid_splits <= 0) return hipSuccess;  // every decode key lies in the shared prefix
   const dim3 grid((unsigned)(a.grid_splits * a.num_seqs), (unsigned)zgroups);
   if (fused)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, R, true, true>), grid, block, 0, stream, a);
   else if (paged)
-    hipLaunchKernelGGL((decode_split_kernel<G, U, true, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, R, true, false>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<G, U, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((decode_split_kernel<G, U, R, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
+}
+
+// One or two kv heads (a tensor-parallel rank's share) spread their keys over the
+// wavefront's four DPP rows (decode_key_rows); otherwise one row per kv head.
+template <int G, int U>
+hipError_t launch_decode_gr(const AttnArgs& a, bool paged, hipStream_t stream) {
+  switch (decode_key_rows(a.num_kv_heads)) {
+    case 4: return launch_decode_g<G, U, 4>(a, paged, stream);
+    case 2: return launch_decode_g<G, U, 2>(a, paged, stream);
+    default: return launch_decode_g<G, U, 1>(a, paged, stream);
+  }
 }
 
 }  // namespace
@@ -287,13 +300,13 @@ hipError_t launch_decode(const AttnArgs& args, int group, bool paged, int max_se
                          hipStream_t stream) {
   if (args.num_seqs <= 0 || max_seqlen_k <= 0) return hipSuccess;
   AttnArgs a = args;
-  a.flat_step = decode_step_keys(group);
+  a.flat_step = decode_flat_step(group, a.num_kv_heads);
   hipError_t err;
   switch (group) {
-    case 1: err = launch_decode_g<1, decode_step_keys(1)>(a, paged, stream); break;
-    case 2: err = launch_decode_g<2, decode_step_keys(2)>(a, paged, stream); break;
-    case 4: err = launch_decode_g<4, decode_step_keys(4)>(a, paged, stream); break;
-    case 8: err = launch_decode_g<8, decode_step_keys(8)>(a, paged, stream); break;
+    case 1: err = launch_decode_gr<1, decode_step_keys(1)>(a, paged, stream); break;
+    case 2: err = launch_decode_gr<2, decode_step_keys(2)>(a, paged, stream); break;
+    case 4: err = launch_decode_gr<4, decode_step_keys(4)>(a, paged, stream); break;
+    case 8: err = launch_decode_gr<8, decode_step_keys(8)>(a, paged, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;

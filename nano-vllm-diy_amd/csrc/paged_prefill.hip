@@ -288,28 +288,39 @@ __device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char*
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) s[rb][mb][rr] = 0.f;
-  // K A operand of half-tile mb, k-block kb, read in batches of kKBatch k-blocks (both
-  // half-tiles) ahead of their MFMAs.
-#ifndef PK_PREFILL_KBATCH
-#define PK_PREFILL_KBATCH 2  // k-blocks per batch of K reads (2, 4 and 8 measured alike)
+  // K A operand of half-tile mb, k-block kb: read kKDepth k-blocks ahead of the MFMAs that
+  // use it, the order pinned by scheduling groups (the compiler's own schedule read each
+  // k-block right before its two MFMAs and waited for it: no read was in flight while an
+  // MFMA ran).
+#ifndef PK_PREFILL_KDEPTH
+#define PK_PREFILL_KDEPTH 2
 #endif
-  constexpr int kKBatch = PK_PREFILL_KBATCH;
+  constexpr int kKDepth = PK_PREFILL_KDEPTH;
+  constexpr int kKBlocks = kHeadDim / 16;
+  bf16x8 ka[kKBlocks][2];
+  const auto read_k = [&](int kb) {
 #pragma unroll
-  for (int k0b = 0; k0b < kHeadDim / 16; k0b += kKBatch) {
-    bf16x8 ka[2][kKBatch];
+    for (int mb = 0; mb < 2; ++mb)
+      ka[kb][mb] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(sK + tl.k[kb] +
+                                                                                   mb * 32 * kRowBytes);
+  };
 #pragma unroll
-    for (int kk = 0; kk < kKBatch; ++kk)
+  for (int kb = 0; kb < kKDepth; ++kb) read_k(kb);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        ka[mb][kk] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(sK + tl.k[k0b + kk] +
-                                                                                     mb * 32 * kRowBytes);
+  for (int kb = 0; kb < kKBlocks; ++kb) {
+    if (kb + kKDepth < kKBlocks) read_k(kb + kKDepth);
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb)
 #pragma unroll
-      for (int kk = 0; kk < kKBatch; ++kk)
+      for (int mb = 0; mb < 2; ++mb)
+        s[rb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kb][mb], qb[rb][kb], s[rb][mb], 0, 0, 0);
+  }
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-          s[rb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[mb][kk], qb[rb][k0b + kk], s[rb][mb], 0, 0, 0);
+  for (int kb = 0; kb < kKDepth; ++kb) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS reads
+#pragma unroll
+  for (int kb = 0; kb < kKBlocks; ++kb) {
+    if (kb + kKDepth < kKBlocks) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * kRowBlocks, 0);  // MFMAs
   }
 
   bf16x8 pb[kRowBlocks][4];
@@ -566,10 +577,15 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
   const LoadLanes ll = load_lanes(a, wave, lane, kTileKeys);
   const TileLanes tl = tile_lanes(lane);
   KvRegs R;
-  if (ntiles > 0) {
-    load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, tbase, ll, R);
-    store_tile_lds(R, KS[0], VS[0], wave, lane);
-  }
+  // The tile loop is entered only from the path that stored tile 0, whose register wait also
+  // covers the Q loads issued before it. (With a path around that store into the loop, the
+  // compiler's wait counting assumed the Q loads could still be in flight in every iteration
+  // and made each k-block's QK MFMA wait for the global loads issued before it -- tile n + 2's
+  // staging loads -- exposing their latency in every tile.)
+  if (ntiles <= 0) lds_barrier();
+  else {
+  load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, tbase, ll, R);
+  store_tile_lds(R, KS[0], VS[0], wave, lane);
   if (ntiles > 1) load_tile_regs<PAGED>(a, b, k0, Lk, g, bt_lane, wave, lane, tbase + TN, ll, R);
   lds_barrier();
   for (int n0 = 0; n0 < ntiles; n0 += 2) {
@@ -596,6 +612,7 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
       if (any) compute_tile(KS[s], VS[s], tl, qb, o, m_i, l_i, t0, lim, full, a.scale_log2, lane);
       lds_barrier();
     }
+  }
   }
 
   after_tiles();
@@ -1124,7 +1141,7 @@ hipError_t launch_prefill_g(const AttnArgs& a, bool paged, bool causal, int max_
   AttnArgs pa = a;
   pa.prefill_qtiles = (max_seqlen_q + TM - 1) / TM;
   pa.pf_slots = device_prefill_slots();
-  pa.flat_step = decode_step_keys(G);  // the decode pieces' step, for the combines in the merge kernel
+  pa.flat_step = decode_flat_step(G, a.num_kv_heads);  // the decode pieces' step, for the merge kernel's combines
   if (paged)
     return causal ? launch_prefill_gpc<G, true, true>(pa, stream) : launch_prefill_gpc<G, true, false>(pa, stream);
   return causal ? launch_prefill_gpc<G, false, true>(pa, stream) : launch_prefill_gpc<G, false, false>(pa, stream);
