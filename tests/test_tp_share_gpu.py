@@ -122,3 +122,28 @@ def test_store_decode_step_bit_identical_at_rank_share(gpu, tp):
     torch.cuda.synchronize()
     assert bits_equal(out, ref)
     assert bits_equal(w.k_cache, kc) and bits_equal(w.v_cache, vc)
+
+
+@pytest.mark.parametrize("tp", SHARES)
+def test_tiny_and_ragged_decode_rows_at_rank_share(gpu, tp):
+    """Decode rows of 1, 2, 3, 5, 7, 9 and 33 keys (fewer keys than a step's rows: with 1 or
+    2 kv heads some DPP rows of a wavefront see no key at all) beside long ragged rows, on the
+    split grid (small batch) and on the flat grid (the same rows in a batch of 128), against
+    the oracle."""
+    import math
+
+    from pagedkv import workloads as W
+
+    hq, hkv = TP_HEADS[tp]
+    tiny = [1, 2, 3, 5, 7, 9, 33, 257, 1000, 4099]
+    # 9 rows of at most 1000 keys: below the flat grid's 32768-key bound, the split grid
+    for n, lens in ((9, tiny[:9]), (128, (tiny * 13)[:128])):
+        g = torch.Generator().manual_seed(300 + tp + n)
+        nb = sum(math.ceil(lk / W.BLOCK_SIZE) for lk in lens)
+        tables = W._pop_tables(lens, torch.randperm(nb, generator=g).tolist())
+        w = W._assemble("tiny", [(1, lk, bt) for lk, bt in zip(lens, tables)], nb, 300 + tp + n, gpu,
+                        heads=(hq, hkv))
+        rows, want = subset_oracle(w, list(range(n)))
+        out = _layer(w)(w.q, w.k, w.v, w.ctx)
+        torch.cuda.synchronize()
+        assert_close_bf16(out[rows], want, f"tiny rows tp={tp} n={n}")
