@@ -256,9 +256,11 @@ def main() -> int:
     ap.add_argument("--cpu-seqs", type=int, default=256, help="sequences in the CPU-baseline sample")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only run 5 cfg3 prefill calls and 5 prefill_steady calls, for rocprofv3 --pmc passes")
-    ap.add_argument("--pmc-probe", action="store_true",
-                    help="only run 5 cfg2 decode calls and 5 copies of 1 GiB (the counter calibration), "
-                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-probe", nargs="?", const="cfg2", default=None,
+                    choices=("cfg2", "cfg4", "decode_serve", "store_16384", "cfg2_tp2", "cfg2_tp8"),
+                    help="only run 5 calls of one workload (default: the cfg2 decode call) and 5 copies "
+                         "of 1 GiB (the counter calibration), for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
+                         "passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the paged-KV path is not sharded across GPUs "
@@ -277,10 +279,10 @@ def main() -> int:
         return 0
     if args.prefill_probe:
         return prefill_probe(dev)
+    if args.pmc_probe:
+        return pmc_probe(dev, args.pmc_probe)
     log("[bench] building cfg2 (256 seqs, Lk ~ U[1024, 8192]) on the GPU")
     w = make_workload("cfg2", dev)
-    if args.pmc_probe:
-        return pmc_probe(w)
     kv_bytes = w.decode_kv_bytes()
     store_bytes = w.store_bytes()
     ctx = w.ctx
@@ -415,24 +417,34 @@ def run_e2e(dev, seed: int = 5) -> dict:
     return res
 
 
-def pmc_probe(w) -> int:
-    """5 decode calls of the cfg2 batch, then 5 device copies of exactly 1 GiB: the copy
-    gives the factor between what FETCH_SIZE / WRITE_SIZE report and the bytes moved."""
+def pmc_probe(dev, name: str) -> int:
+    """5 calls of one workload's path, then 5 device copies of exactly 1 GiB: the copy gives
+    the factor between what FETCH_SIZE / WRITE_SIZE report and the bytes moved. Workloads:
+    cfg2 / cfg2_tp2 / cfg2_tp8 (the decode call at the full heads or a tensor-parallel
+    rank's share), cfg4 (the shared-prefix call), decode_serve (128 sequences of 100-2048
+    keys: the flat grid), store_16384 (store_kvcache of a 16384-token prefill step)."""
     import torch
 
-    import pagedkv
+    from pagedkv.workloads import TP_HEADS, make_workload
 
-    out = torch.empty_like(w.q)
+    if name == "store_16384":
+        fn, nbytes = store_call(dev, 16384)
+        info = {"store_bytes": nbytes}
+    else:
+        base, _, tp = name.partition("_tp")
+        w = make_workload(base, dev, heads=TP_HEADS[int(tp) if tp else 1])
+        fn = attention_call(w)
+        info = {"kv_bytes": w.decode_kv_bytes()}
+        if base == "cfg4":
+            info["unique_bytes"] = w.decode_unique_kv_bytes()
     for _ in range(5):
-        pagedkv.varlen_attention(w.q, w.k_cache, w.v_cache, w.cu_seqlens_q, w.cu_seqlens_k, 1,
-                                 w.max_seqlen_k, SCALE, True, w.block_tables, out=out,
-                                 cached_prefix_keys=w.shared_prefix_keys)
-    src = torch.ones(1 << 29, dtype=torch.int16, device=w.q.device)
+        fn()
+    src = torch.ones(1 << 29, dtype=torch.int16, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_probe": "done", "kv_bytes": w.decode_kv_bytes(), "copy_bytes": 1 << 30}), flush=True)
+    print(json.dumps({"pmc_probe": name, **info, "copy_bytes": 1 << 30}), flush=True)
     return 0
 
 
@@ -629,6 +641,15 @@ def extra_configs(dev, w2):
                                "heads": f"{hq}q/{hkv}kv", "kv_bytes": wt.decode_kv_bytes()}
         del wt
         torch.cuda.empty_cache()
+
+    wv = make_workload("decode_serve", dev)
+    ms, _ = timed_launches(attention_call(wv), 20)
+    res["decode_serve_128"] = {"ms": round(ms, 5), "GB/s": round(wv.decode_kv_bytes() / ms / 1e6, 1),
+                               "frac": round(wv.decode_kv_bytes() / ms / 1e6 / HBM_PEAK_GBS, 4),
+                               "kv_bytes": wv.decode_kv_bytes(),
+                               "batch": "128 sequences of U[100, 2048] keys (the serving run's decode steps): "
+                                        "flat grid + combine"}
+    del wv
 
     log("[bench] producer")
     for n in (256, 16384):

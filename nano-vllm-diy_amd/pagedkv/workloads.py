@@ -36,7 +36,7 @@ ROW_BYTES = HKV * HEAD_DIM * 2                     # one token row of K (or V), 
 # src/config/runner_config.py:12,40): (Hq / tp, Hkv / tp).
 TP_HEADS = {1: (16, 8), 2: (8, 4), 4: (4, 2), 8: (2, 1)}
 
-WORKLOADS = ("cfg1_store", "cfg1_decode", "cfg2", "cfg3", "cfg4", "prefill_steady")
+WORKLOADS = ("cfg1_store", "cfg1_decode", "cfg2", "cfg3", "cfg4", "prefill_steady", "decode_serve")
 
 
 @dataclass
@@ -233,7 +233,8 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
     if hq <= 0 or hkv <= 0 or hq % hkv:
         raise ValueError(f"heads {heads}: Hq must be a positive multiple of Hkv")
     kw = {"heads": (hq, hkv)}
-    cfg_seed = {"cfg1_store": 1, "cfg1_decode": 1, "cfg2": 2, "cfg3": 3, "cfg4": 4, "prefill_steady": 5}[name]
+    cfg_seed = {"cfg1_store": 1, "cfg1_decode": 1, "cfg2": 2, "cfg3": 3, "cfg4": 4, "prefill_steady": 5,
+                "decode_serve": 9}[name]
     seed = cfg_seed if seed is None else seed
     host = torch.Generator()
     host.manual_seed(seed)
@@ -261,6 +262,17 @@ def make_workload(name: str, device="cpu", seed: int | None = None,
         pool = torch.randperm(nb, generator=host).tolist()
         tables = _pop_tables(lks, pool)
         return _assemble(name, [(1, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 2, device,
+                         unique_blocks=nb, **kw)
+
+    if name == "decode_serve":
+        # the serving run's decode steps: 128 live sequences (the scheduler's cap,
+        # scheduler.py:37) of prompt + generated tokens, contexts U[100, 2048]
+        s = 128 if num_seqs is None else num_seqs
+        lks = _uniform(host, 100, 2048, s)
+        nb = sum(math.ceil(lk / BLOCK_SIZE) for lk in lks)
+        pool = torch.randperm(nb, generator=host).tolist()
+        tables = _pop_tables(lks, pool)
+        return _assemble(name, [(1, lk, bt) for lk, bt in zip(lks, tables)], nb, seed * 1000 + 9, device,
                          unique_blocks=nb, **kw)
 
     if name == "cfg3":

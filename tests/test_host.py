@@ -108,6 +108,41 @@ def test_workloads_are_deterministic_and_well_formed():
         assert a.k.is_contiguous() and a.q.is_contiguous()
 
 
+def test_workloads_at_tensor_parallel_shares():
+    """heads=(Hq, Hkv) keeps lengths, block tables and slots, and shrinks the rows: q
+    (N, Hq, D), k and v (N, Hkv, D) with v a view of the (Hq + 2 Hkv) D qkv row, caches
+    (NB, BS, Hkv, D), and the algorithmic bytes scale with Hkv."""
+    from pagedkv.workloads import TP_HEADS
+
+    assert TP_HEADS == {1: (16, 8), 2: (8, 4), 4: (4, 2), 8: (2, 1)}
+    for name in ("cfg2", "cfg3", "cfg4"):
+        full = make_workload(name, "cpu", num_seqs=5)
+        for tp, (hq, hkv) in TP_HEADS.items():
+            w = make_workload(name, "cpu", num_seqs=5, heads=(hq, hkv))
+            assert w.k_lens == full.k_lens and torch.equal(w.block_tables, full.block_tables)
+            assert torch.equal(w.slot_mapping, full.slot_mapping)
+            assert w.q.shape[1:] == (hq, HEAD_DIM) and w.k.shape[1:] == (hkv, HEAD_DIM)
+            assert w.k_cache.shape[1:] == (BLOCK_SIZE, hkv, HEAD_DIM)
+            assert w.v.stride(0) == (hq + 2 * hkv) * HEAD_DIM
+            assert w.decode_kv_bytes() * tp == full.decode_kv_bytes()
+            assert w.prefill_flops() * tp == full.prefill_flops()
+    with pytest.raises(ValueError):
+        make_workload("cfg2", "cpu", num_seqs=2, heads=(6, 4))
+
+
+def test_shared_prefix_unique_bytes():
+    """cfg4: unique bytes are the distinct keys, (2048 + sum of the suffixes) * 2R; the
+    whole-block figure counts the blocks that hold them; logical bytes every sequence's keys."""
+    w = make_workload("cfg4", "cpu")
+    R = HKV * HEAD_DIM * 2
+    suffix = [lk - 2048 for lk in w.k_lens]
+    assert all(256 <= x <= 1024 for x in suffix)
+    assert w.decode_unique_kv_bytes() == (2048 + sum(suffix)) * 2 * R
+    blocks = 8 + sum(math.ceil(x / BLOCK_SIZE) for x in suffix)
+    assert w.decode_unique_block_bytes() == blocks * BLOCK_SIZE * 2 * R
+    assert w.decode_kv_bytes() == sum(w.k_lens) * 2 * R
+
+
 @pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4"])
 def test_block_tables_and_slots(name):
     w = make_workload(name, "cpu", num_seqs=6)
