@@ -405,14 +405,23 @@ int attention_impl(const void* q, int64_t q_row_stride, const void* k, const voi
   }
 
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (a.prefix_keys > 0) {
-    int rc = hip_status(pk::launch_shared_prefix(a, group, s), "shared-prefix launch");
-    if (rc != PK_OK) return rc;
-  }
   // with prefill rows the decode partials are merged by the prefill merge kernel, which the
   // call launches anyway (one launch fewer)
   a.combine_in_merge = max_seqlen_q > 1;
-  int rc = hip_status(pk::launch_decode(a, group, paged, max_seqlen_k, s), "decode launch");
+  int rc = PK_OK;
+  hipError_t e = hipSuccess;
+  if (a.prefix_keys > 0 && pk::launch_shared_prefix_flat(a, group, s, &e)) {
+    // the shared-prefix work and the flat decode grid in one launch, then the combine
+    rc = hip_status(e, "shared-prefix + flat decode launch");
+    if (rc != PK_OK) return rc;
+    rc = hip_status(pk::launch_decode_combine(a, group, s), "decode combine launch");
+  } else {
+    if (a.prefix_keys > 0) {
+      rc = hip_status(pk::launch_shared_prefix(a, group, s), "shared-prefix launch");
+      if (rc != PK_OK) return rc;
+    }
+    rc = hip_status(pk::launch_decode(a, group, paged, max_seqlen_k, s), "decode launch");
+  }
   if (rc != PK_OK) return rc;
   if (max_seqlen_q > 1)
     rc = hip_status(pk::launch_prefill(a, group, paged, causal != 0, max_seqlen_q, s), "prefill launch");

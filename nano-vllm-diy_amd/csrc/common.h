@@ -75,6 +75,15 @@ struct AttnArgs {
   int32_t prefix_stride;        // partial units per sequence of the prefix chunk partials (chunk j of
                                 // sequence b at unit b * prefix_stride + j)
   int32_t sp_replicas;          // shared-prefix kernel: work-groups per window of sequences (set by its launch)
+  // One launch for the shared-prefix work and the flat decode grid (set by that launch):
+  // work-groups [0, sp_groups) take the (chunk, kv head, window) prefix work and then
+  // sp_tail flat groups each, the sp_decode work-groups after them sp_per flat groups each;
+  // a flat group is sp_quads wavefronts (4 kv heads each, or 4 / R with key rows).
+  int32_t sp_groups;
+  int32_t sp_decode;
+  int32_t sp_per;
+  int32_t sp_tail;
+  int32_t sp_quads;
   // chunked-prefill work plan (workspace): a work item is (sequence, kv head, query tile,
   // key-tile range); items of one query tile that was split over several key ranges write
   // fp32 partials that a merge pass combines.
@@ -201,6 +210,12 @@ hipError_t launch_decode(const AttnArgs& a, int group, bool paged, int max_seqle
 // Decode rows over their shared-prefix keys (a.prefix_keys > 0): MFMA tiles of the query rows
 // of every sequence whose block table names the same blocks, one partial per chunk.
 hipError_t launch_shared_prefix(const AttnArgs& a, int group, hipStream_t stream);
+// The shared-prefix work and the flat decode grid over the keys after the prefix in one launch
+// (when the flat grid is on and the kv heads divide into the work-group's wavefronts);
+// returns false (nothing launched) when the separate launches apply.
+bool launch_shared_prefix_flat(AttnArgs& a, int group, hipStream_t stream, hipError_t* err);
+// The decode launch's combine pass alone (after launch_shared_prefix_flat).
+hipError_t launch_decode_combine(const AttnArgs& a, int group, hipStream_t stream);
 // bf16-MFMA attention over sequences with more than one query row.
 hipError_t launch_prefill(const AttnArgs& a, int group, bool paged, bool causal,
                           int max_seqlen_q, hipStream_t stream);

@@ -97,9 +97,13 @@ __device__ __forceinline__ int scalar_block_id(const int32_t* row, int j) {
 // by the buffer's range instead of clamped (a row's key past t_end reads zeros, finite,
 // masked to p = 0 by consume): the row offset is per lane, which a scalar offset cannot
 // carry.
+// live == false: a prefetch past the unit's last step, whose values are never used; its loads
+// go out (the pipeline's wait counts stay exact) over an empty buffer range, so they return
+// zeros without touching memory (a re-read of the last step, streamed past L2, came back from
+// HBM: one extra step per unit, ~15% of the bytes of a short flat-grid piece).
 template <int U, int R, bool PAGED, bool STREAM, bool FUSED>
 __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_k, uint32_t lane_v, int b, int k0, int t,
-                                            int t_end, u32x4 (&kr)[U], u32x4 (&vr)[U]) {
+                                            int t_end, bool live, u32x4 (&kr)[U], u32x4 (&vr)[U]) {
   const uint16_t* kp;
   const uint16_t* vp;
   if constexpr (PAGED) {
@@ -117,15 +121,15 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_k, 
   const uint32_t k_row_bytes = (uint32_t)a.k_row_stride * 2u;
   const uint32_t v_row_bytes = (uint32_t)a.v_row_stride * 2u;
   if constexpr (R == 1) {
-    const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, (uint32_t)U * k_row_bytes);
-    const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, (uint32_t)U * v_row_bytes);
+    const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, live ? (uint32_t)U * k_row_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, live ? (uint32_t)U * v_row_bytes : 0u);
     const int last = t_end - 1 - t;
 #pragma unroll
     for (int u = 0; u < U; ++u) kr[u] = load16<STREAM>(kr_rs, lane_k, __umul24((uint32_t)min(u, last), k_row_bytes));
 #pragma unroll
     for (int u = 0; u < U; ++u) vr[u] = load16<STREAM>(vr_rs, lane_v, __umul24((uint32_t)min(u, last), v_row_bytes));
   } else {
-    const uint32_t rows = (uint32_t)min(U * R, t_end - t);  // keys of the step that exist
+    const uint32_t rows = live ? (uint32_t)min(U * R, t_end - t) : 0u;  // keys of the step that exist
     const __amdgpu_buffer_rsrc_t kr_rs = row_rsrc(kp, rows * k_row_bytes);
     const __amdgpu_buffer_rsrc_t vr_rs = row_rsrc(vp, rows * v_row_bytes);
 #pragma unroll
@@ -137,8 +141,8 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_k, 
 
 // Keys [t_begin, t_end) of one split through a two-stage software pipeline: the loads of
 // step n+1 are in flight while step n is consumed. The prefetch is unconditional (past
-// t_end it re-reads the current step, which hits in cache) so the code is straight-line
-// and the wait counts stay exact. The scheduling barriers keep each step's loads together
+// t_end it is issued over an empty range) so the code is straight-line and the wait counts
+// stay exact. The scheduling barriers keep each step's loads together
 // ahead of its math: otherwise the scheduler sinks every load next to its first use to
 // save registers, which serialises their latency.
 template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, class Pre>
@@ -220,16 +224,18 @@ __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs&
   constexpr int S = U * R;  // keys per step
   const float c2 = a.scale_log2;
   u32x4 kA[U], vA[U], kB[U], vB[U];
-  issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t_begin, t_end, kA, vA);
+  issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t_begin, t_end, true, kA, vA);
   pre();  // q (loaded or computed) while the first K/V loads are in flight
   for (int t = t_begin; t < t_end; t += 2 * S) {
     const int t1 = t + S;
-    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t1 < t_end ? t1 : t, t_end, kB, vB);
+    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t1 < t_end ? t1 : t, t_end, t1 < t_end, kB,
+                                            vB);
     __builtin_amdgcn_sched_barrier(0);
     consume<G, U, R>(st, c2, t, t_end, j, kA, vA);
     if (t1 >= t_end) break;
     const int t2 = t1 + S;
-    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t2 < t_end ? t2 : t1, t_end, kA, vA);
+    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t2 < t_end ? t2 : t1, t_end, t2 < t_end, kA,
+                                            vA);
     __builtin_amdgcn_sched_barrier(0);
     consume<G, U, R>(st, c2, t1, t_end, j, kB, vB);
   }
@@ -439,6 +445,94 @@ __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
             r2 = __builtin_amdgcn_readlane(v, 47);
   const int row = lane >> 4;
   return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
+// Flat decode grid: the decode keys of the batch -- per decode sequence b the c_b keys after its
+// shared prefix (all of them without one) -- are laid end to end in sequence order (the key
+// line: sequence b from position pos_b = c_0 + ... + c_{b-1}) and cut into W = flat_groups
+// runs of `chunk` keys, so that every work-group streams the same number of K/V rows
+// whatever the length mix. A pipeline step (U R keys at a multiple of U R after the prefix)
+// belongs to the run holding its first key, so sequence b has a piece in runs w0(b) .. w1(b).
+// Piece (b, w) is work-group u = b + w and partial unit flat_unit0 + u: unique, because the
+// runs and the sequences both tile the line in order (b + w1(b) < b' + w0(b') for b < b').
+// Groups u = 0 .. W + num_seqs: those between two sequences' ranges hold no piece, and the
+// last one records chunk and every pos_b for the combine. chunk = max(flat_min_chunk,
+// ceil(T / W) rounded up to the step), T = the line's length. One wavefront holds every
+// sequence's bounds (num_seqs < 64 * kFlatSlots), forms the line with a wavefront prefix sum
+// and finds its group's sequence with one ballot per slot.
+constexpr int kFlatSlots = 8;
+
+// One wavefront's share of flat work-group u (its piece, for the kv heads from g_first):
+// the flat decode kernel runs it with u = its work-group index, the shared-prefix launch that
+// carries the flat grid with u numbered across its decode work-groups. `recorder`: this
+// wavefront records the line (chunk and every pos_b) for the combine if u is the last group.
+template <int G, int U, int R, bool PAGED, bool FUSED>
+__device__ __forceinline__ void flat_decode_piece(const AttnArgs& a, int u, int g_first, int lane, bool recorder) {
+  constexpr int ST = U * R;  // keys per pipeline step: the line's step
+  const int n = a.num_seqs;
+  // lane l, slot s: sequence e = l + 64 s
+  int kb[kFlatSlots], qb[kFlatSlots], lk[kFlatSlots], cnt[kFlatSlots], pos[kFlatSlots];
+  int T = 0;
+#pragma unroll
+  for (int s = 0; s < kFlatSlots; ++s) {
+    kb[s] = qb[s] = lk[s] = cnt[s] = pos[s] = 0;
+    if (64 * s < n) {
+      const int e = lane + 64 * s;
+      if (e < n) {
+        kb[s] = a.cu_k[e];
+        qb[s] = a.cu_q[e];
+        const int k1 = a.cu_k[e + 1], q1 = a.cu_q[e + 1];
+        lk[s] = min(k1 - kb[s], a.max_seqlen_k);
+        const int pb = max(0, min(a.prefix_keys, lk[s]));
+        cnt[s] = (q1 - qb[s] == 1 && lk[s] > 0) ? lk[s] - pb : 0;  // decode keys after the prefix
+      }
+      const int incl = wave_inclusive_sum(cnt[s], lane);
+      pos[s] = T + incl - cnt[s];
+      T += __builtin_amdgcn_readlane(incl, kWave - 1);
+    }
+  }
+  const int per = (T + a.flat_groups - 1) / a.flat_groups;
+  const int chunk = max(a.flat_min_chunk, (per + ST - 1) / ST * ST);
+  // the decode sequence with b + w0(b) <= u <= b + w1(b), if any
+  int b = -1, q0 = 0, k0 = 0, Lk = 0, p0 = 0, cb = 0;
+#pragma unroll
+  for (int s = 0; s < kFlatSlots; ++s) {
+    if (64 * s < n) {
+      const int e = lane + 64 * s;
+      const int w0 = pos[s] / chunk;
+      const int w1 = (pos[s] + (cnt[s] - 1) / ST * ST) / chunk;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(cnt[s] > 0 && e + w0 <= u && u <= e + w1);
+      if (m) {
+        const int j = __builtin_ctzll(m);
+        b = 64 * s + j;
+        q0 = __builtin_amdgcn_readlane(qb[s], j);
+        k0 = __builtin_amdgcn_readlane(kb[s], j);
+        Lk = __builtin_amdgcn_readlane(lk[s], j);
+        p0 = __builtin_amdgcn_readlane(pos[s], j);
+        cb = __builtin_amdgcn_readlane(cnt[s], j);
+      }
+    }
+  }
+  if (b < 0) {
+    // The last work-group holds no piece (b + w1(b) <= num_seqs - 1 + W - 1): it records the
+    // line for the combine. (Recorded here, after the search, so that its stores precede no
+    // block-table read on any path: the compiler then reads the table with scalar loads.)
+    if (u == a.flat_groups + n && recorder) {
+      if (lane == 0) a.flat_meta[0] = chunk;
+#pragma unroll
+      for (int s = 0; s < kFlatSlots; ++s)
+        if (lane + 64 * s < n) a.flat_meta[1 + lane + 64 * s] = pos[s];
+    }
+    return;
+  }
+  const int Pb = Lk - cb;                                // keys of the shared prefix
+  const int F0 = (u - b) * chunk, F1 = F0 + chunk;       // this run, on the line
+  const int t_begin = Pb + (F0 > p0 ? (F0 - p0 + ST - 1) / ST * ST : 0);
+  const int t_end = min(Lk, Pb + (F1 - p0 + ST - 1) / ST * ST);
+  // the sequence's first and last steps in one run and no prefix partial: this piece is all of it
+  const bool direct = Pb == 0 && p0 / chunk == (p0 + (cb - 1) / ST * ST) / chunk;
+  decode_unit<G, U, R, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
+                                     ((int64_t)a.flat_unit0 + u) * a.num_heads);
 }
 
 // Merge the per-split partials of one (sequence, head). A separate pass (rather than a "last

@@ -100,96 +100,19 @@ __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_split_kernel(co
                                      ((int64_t)b * a.max_splits + slot) * a.num_heads);
 }
 
-// Flat mode: the decode keys of the batch -- per decode sequence b the c_b keys after its
-// shared prefix (all of them without one) -- are laid end to end in sequence order (the key
-// line: sequence b from position pos_b = c_0 + ... + c_{b-1}) and cut into W = flat_groups
-// runs of `chunk` keys, so that every work-group streams the same number of K/V rows
-// whatever the length mix (the split grid gives each sequence whole splits: its last split
-// is ragged, short sequences leave many work-groups empty, and prefill rows of a mixed batch
-// or keys past max_seqlen_k take no place on the line). A pipeline step (U keys at a multiple
-// of U after the prefix) belongs to the run holding its first key, so sequence b has a piece
-// in runs w0(b) .. w1(b) (the runs of its first and last steps). Piece (b, w) is work-group
-// u = b + w and partial unit flat_unit0 + u: the index is unique because the runs and the
-// sequences both tile the line in order, so b + w1(b) < b' + w0(b') for b < b'. The grid has
-// W + num_seqs + 1 work-groups: those whose index falls between two sequences' ranges exit at
-// once, and the last one records chunk and every pos_b for the combine. (174 VGPRs for G = 2,
-// two wavefronts per SIMD: the 1024-work-group grid of two-wavefront groups fits 4 per CU.)
-// chunk = max(flat_min_chunk, ceil(T / W) rounded up to U), T = the line's length. One
-// wavefront holds every sequence's bounds (num_seqs < 64 * kFlatSlots), forms the line with a
-// wavefront prefix sum and finds the work-group's sequence with one ballot per slot.
-constexpr int kFlatSlots = 8;
-
+// Flat mode (flat_decode_piece): the batch's decode keys laid end to end and cut into
+// flat_groups runs of equal length, one work-group per (sequence, run) piece, so that every
+// work-group streams the same number of K/V rows whatever the length mix (the split grid
+// gives each sequence whole splits: its last split is ragged, short sequences leave many
+// work-groups empty, and prefill rows of a mixed batch or keys past max_seqlen_k take no
+// place on the line). (174 VGPRs for G = 2, two wavefronts per SIMD: the 1024-work-group
+// grid of two-wavefront groups fits 4 per CU.)
 template <int G, int U, int R, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(kWave* kDecodeMaxWaves) void decode_flat_kernel(const AttnArgs a) {
-  constexpr int ST = U * R;  // keys per pipeline step: the line's step
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g_first = (blockIdx.y * (blockDim.x / kWave) + wave) * (4 / R);
-  const int n = a.num_seqs;
-  // lane l, slot s: sequence e = l + 64 s
-  int kb[kFlatSlots], qb[kFlatSlots], lk[kFlatSlots], cnt[kFlatSlots], pos[kFlatSlots];
-  int T = 0;
-#pragma unroll
-  for (int s = 0; s < kFlatSlots; ++s) {
-    kb[s] = qb[s] = lk[s] = cnt[s] = pos[s] = 0;
-    if (64 * s < n) {
-      const int e = lane + 64 * s;
-      if (e < n) {
-        kb[s] = a.cu_k[e];
-        qb[s] = a.cu_q[e];
-        const int k1 = a.cu_k[e + 1], q1 = a.cu_q[e + 1];
-        lk[s] = min(k1 - kb[s], a.max_seqlen_k);
-        const int pb = max(0, min(a.prefix_keys, lk[s]));
-        cnt[s] = (q1 - qb[s] == 1 && lk[s] > 0) ? lk[s] - pb : 0;  // decode keys after the prefix
-      }
-      const int incl = wave_inclusive_sum(cnt[s], lane);
-      pos[s] = T + incl - cnt[s];
-      T += __builtin_amdgcn_readlane(incl, kWave - 1);
-    }
-  }
-  const int per = (T + a.flat_groups - 1) / a.flat_groups;
-  const int chunk = max(a.flat_min_chunk, (per + ST - 1) / ST * ST);
-  const int u = blockIdx.x;
-  // the decode sequence with b + w0(b) <= u <= b + w1(b), if any
-  int b = -1, q0 = 0, k0 = 0, Lk = 0, p0 = 0, cb = 0;
-#pragma unroll
-  for (int s = 0; s < kFlatSlots; ++s) {
-    if (64 * s < n) {
-      const int e = lane + 64 * s;
-      const int w0 = pos[s] / chunk;
-      const int w1 = (pos[s] + (cnt[s] - 1) / ST * ST) / chunk;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(cnt[s] > 0 && e + w0 <= u && u <= e + w1);
-      if (m) {
-        const int j = __builtin_ctzll(m);
-        b = 64 * s + j;
-        q0 = __builtin_amdgcn_readlane(qb[s], j);
-        k0 = __builtin_amdgcn_readlane(kb[s], j);
-        Lk = __builtin_amdgcn_readlane(lk[s], j);
-        p0 = __builtin_amdgcn_readlane(pos[s], j);
-        cb = __builtin_amdgcn_readlane(cnt[s], j);
-      }
-    }
-  }
-  if (b < 0) {
-    // The last work-group holds no piece (b + w1(b) <= num_seqs - 1 + W - 1): it records the
-    // line for the combine. (Recorded here, after the search, so that its stores precede no
-    // block-table read on any path: the compiler then reads the table with scalar loads.)
-    if (u == a.flat_groups + n && blockIdx.y == 0 && wave == 0) {
-      if (lane == 0) a.flat_meta[0] = chunk;
-#pragma unroll
-      for (int s = 0; s < kFlatSlots; ++s)
-        if (lane + 64 * s < n) a.flat_meta[1 + lane + 64 * s] = pos[s];
-    }
-    return;
-  }
-  const int Pb = Lk - cb;                                // keys of the shared prefix
-  const int F0 = (u - b) * chunk, F1 = F0 + chunk;       // this run, on the line
-  const int t_begin = Pb + (F0 > p0 ? (F0 - p0 + ST - 1) / ST * ST : 0);
-  const int t_end = min(Lk, Pb + (F1 - p0 + ST - 1) / ST * ST);
-  // the sequence's first and last steps in one run and no prefix partial: this piece is all of it
-  const bool direct = Pb == 0 && p0 / chunk == (p0 + (cb - 1) / ST * ST) / chunk;
-  decode_unit<G, U, R, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
-                                     ((int64_t)a.flat_unit0 + u) * a.num_heads);
+  flat_decode_piece<G, U, R, PAGED, FUSED>(a, blockIdx.x, g_first, lane, blockIdx.y == 0 && wave == 0);
 }
 
 // EAGER > 0 (small split-grid batches without a shared prefix, max_splits <= EAGER): the
@@ -296,6 +219,23 @@ FlatDecodePlan decode_flat_plan(int num_seqs, int max_seqlen_k) {
   return p;
 }
 
+hipError_t launch_decode_combine(const AttnArgs& a, int group, hipStream_t stream) {
+  (void)group;
+  if (a.num_seqs <= 0) return hipSuccess;
+  // (a call with prefill rows merges the decode partials in its prefill merge kernel)
+  if ((a.max_splits > 1 || a.flat_groups > 0) && !a.combine_in_merge) {
+    const dim3 grid((unsigned)a.num_heads, (unsigned)a.num_seqs), block(kCombineThreads);
+    if (!eager_combine(a))
+      hipLaunchKernelGGL((decode_combine_kernel<0>), grid, block, 0, stream, a);
+    else if (a.max_splits <= 32)
+      hipLaunchKernelGGL((decode_combine_kernel<32>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_combine_kernel<kCombineFast>), grid, block, 0, stream, a);
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_decode(const AttnArgs& args, int group, bool paged, int max_seqlen_k,
                          hipStream_t stream) {
   if (args.num_seqs <= 0 || max_seqlen_k <= 0) return hipSuccess;
@@ -310,18 +250,7 @@ hipError_t launch_decode(const AttnArgs& args, int group, bool paged, int max_se
     default: return hipErrorInvalidValue;
   }
   if (err != hipSuccess) return err;
-  // (a call with prefill rows merges the decode partials in its prefill merge kernel)
-  if ((a.max_splits > 1 || a.flat_groups > 0) && !a.combine_in_merge) {
-    const dim3 grid((unsigned)a.num_heads, (unsigned)a.num_seqs), block(kCombineThreads);
-    if (!eager_combine(a))
-      hipLaunchKernelGGL((decode_combine_kernel<0>), grid, block, 0, stream, a);
-    else if (a.max_splits <= 32)
-      hipLaunchKernelGGL((decode_combine_kernel<32>), grid, block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((decode_combine_kernel<kCombineFast>), grid, block, 0, stream, a);
-    err = hipGetLastError();
-  }
-  return err;
+  return launch_decode_combine(a, group, stream);
 }
 
 }  // namespace pk

@@ -925,7 +925,7 @@ __global__ __launch_bounds__(kMergeThreads) __attribute__((amdgpu_waves_per_eu(1
 // leads in sequence order, so all replicas of a window see the same group list. Member ranks
 // come from an atomic counter; they only place the rows inside the work-group's own tiles.
 template <int G>
-__global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_kernel(const AttnArgs a) {
+__device__ __forceinline__ void shared_prefix_work(const AttnArgs& a, const int c, const int g, const int z) {
   static_assert(kRowBlocks == 1, "one 32-row block per wavefront");
   constexpr int D = kHeadDim;
   constexpr int MC = kPrefillRows / G;  // sequences per window (and rows of one head per tile set)
@@ -948,13 +948,10 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
   const int CK = a.prefix_chunk;
   const int Cb = CK / BS;
   const int S = a.num_seqs;
-  // grid (chunk, kv head, window x replicas): work-groups go to the XCDs round-robin by linear
-  // id, so with z slowest the first replica of every (chunk, head) spreads over all of them
-  const int c = blockIdx.x;
-  const int g = blockIdx.y;
+  // work-group (chunk c, kv head g, z = window x replicas + replica)
   const int nrep = a.sp_replicas;
-  const int win = (int)blockIdx.z / nrep;
-  const int rep = (int)blockIdx.z - win * nrep;
+  const int win = z / nrep;
+  const int rep = z - win * nrep;
   const int s0 = win * MC;
   const int nwin = min(MC, S - s0);
 
@@ -1113,6 +1110,47 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
   }
 }
 
+// grid (chunk, kv head, window x replicas): work-groups go to the XCDs round-robin by linear
+// id, so with z slowest the first replica of every (chunk, head) spreads over all of them
+template <int G>
+__global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_kernel(const AttnArgs a) {
+  shared_prefix_work<G>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// The shared-prefix work and the flat decode grid over the keys after the prefix in one
+// launch. Run back to back, the prefix kernel -- a chain of dependent steps in a few dozen
+// work-groups (bounds, grouping, member list, q rows, tiles, partials), most of the GPU idle
+// -- and the flat grid, which streams the suffixes on every CU, add up; here the first
+// sp_groups work-groups take the prefix work (one replica per window) and then sp_tail flat
+// groups each, and the sp_decode work-groups after them sp_per flat groups each, as many as
+// the CUs left beside the prefix work hold at once. The two kinds write disjoint partial slots
+// (prefix chunks, then the flat pieces), merged by the combine pass as before. A work-group's
+// eight wavefronts take its flat groups sp_quads at a time (one flat group = the kv heads of
+// sp_quads wavefronts); the flat grid's groups are numbered across the work-groups.
+template <int G, int U, int R>
+__global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_flat_kernel(const AttnArgs a) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int blk = blockIdx.x;
+  int first, count;  // this work-group's flat groups
+  if (blk < a.sp_groups) {
+    const int c = blk % a.prefix_slots;
+    const int rest = blk / a.prefix_slots;
+    shared_prefix_work<G>(a, c, rest % a.num_kv_heads, rest / a.num_kv_heads);
+    first = a.sp_decode * a.sp_per + blk * a.sp_tail;
+    count = a.sp_tail;
+  } else {
+    first = (blk - a.sp_groups) * a.sp_per;
+    count = a.sp_per;
+  }
+  const int j = wave / a.sp_quads;  // this wavefront's flat group, and its kv-head quad in it
+  const int qd = wave - j * a.sp_quads;
+  const int u = first + j;
+  if (j < count && u <= a.flat_groups + a.num_seqs)
+    flat_decode_piece<G, U, R, true, false>(a, u, qd * (4 / R), lane, qd == 0);
+}
+
 
 int device_prefill_slots() {
   static int cached[64];
@@ -1162,6 +1200,67 @@ void launch_shared_prefix_g(AttnArgs a, hipStream_t stream) {
   hipLaunchKernelGGL(shared_prefix_kernel<G>,
                      dim3((unsigned)a.prefix_slots, (unsigned)a.num_kv_heads, (unsigned)(windows * a.sp_replicas)),
                      dim3(kPrefillThreads), 0, stream, a);
+}
+
+template <int G, int U, int R>
+void launch_shared_prefix_flat_g(const AttnArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((shared_prefix_flat_kernel<G, U, R>), dim3((unsigned)(a.sp_groups + a.sp_decode)),
+                     dim3(kPrefillThreads), 0, stream, a);
+}
+
+template <int G>
+void launch_shared_prefix_flat_gr(const AttnArgs& a, hipStream_t stream) {
+  constexpr int U = decode_step_keys(G);
+  switch (decode_key_rows(a.num_kv_heads)) {
+    case 4: launch_shared_prefix_flat_g<G, U, 4>(a, stream); break;
+    case 2: launch_shared_prefix_flat_g<G, U, 2>(a, stream); break;
+    default: launch_shared_prefix_flat_g<G, U, 1>(a, stream); break;
+  }
+}
+
+bool launch_shared_prefix_flat(AttnArgs& a, int group, hipStream_t stream, hipError_t* err) {
+  *err = hipSuccess;
+  if (a.num_seqs <= 0 || a.prefix_keys <= 0 || a.prefix_slots <= 0 || a.flat_groups <= 0) return false;
+  if (!a.block_table || !a.part_o || !a.part_ml || a.num_seqs > kSharedPrefixMaxSeqs ||
+      a.prefix_chunk % a.block_size != 0 || a.prefix_chunk / a.block_size > kSharedPrefixMaxChunkBlocks ||
+      a.prefix_slots > kCombineMaxSplits)
+    return false;
+  const int nh = 4 / decode_key_rows(a.num_kv_heads);           // kv heads per wavefront
+  const int quads = (a.num_kv_heads + nh - 1) / nh;              // wavefronts per flat group
+  if (kPrefillWaves % quads != 0) return false;
+  const int per = kPrefillWaves / quads;                         // flat groups per work-group
+  const int MC = kPrefillRows / group;
+  const int windows = (a.num_seqs + MC - 1) / MC;
+  const int64_t P = (int64_t)a.prefix_slots * a.num_kv_heads * windows;
+  const int cus = device_prefill_slots();                        // one work-group per CU
+  if (P >= cus / 2) return false;                                // little room left for the suffixes
+  // decode work-groups fill the CUs beside the prefix ones; those take half a share after
+  // their prefix work. The flat grid shrinks to the groups these hold (never grows: the
+  // workspace's partial slots are sized for the flat plan's grid).
+  const int tail = per / 2;
+  const int D = cus - (int)P;
+  const int64_t total = (int64_t)D * per + P * tail;             // flat groups, recorder included
+  const int W = (int)std::min<int64_t>(a.flat_groups, total - a.num_seqs - 1);
+  if (W < 2) return false;
+  a.flat_groups = W;
+  a.sp_replicas = 1;
+  a.sp_groups = (int)P;
+  a.sp_decode = D;
+  a.sp_per = per;
+  a.sp_tail = tail;
+  a.sp_quads = quads;
+  a.flat_step = decode_flat_step(group, a.num_kv_heads);
+  // the decode launch's partial-store policy (kStoreThroughBytes), on this grid's units
+  a.store_through = ((int64_t)a.num_seqs + a.flat_groups) * a.num_heads * kHeadDim * 4 > kStoreThroughBytes;
+  switch (group) {
+    case 1: launch_shared_prefix_flat_gr<1>(a, stream); break;
+    case 2: launch_shared_prefix_flat_gr<2>(a, stream); break;
+    case 4: launch_shared_prefix_flat_gr<4>(a, stream); break;
+    case 8: launch_shared_prefix_flat_gr<8>(a, stream); break;
+    default: *err = hipErrorInvalidValue; return true;
+  }
+  *err = hipGetLastError();
+  return true;
 }
 
 hipError_t launch_shared_prefix(const AttnArgs& a, int group, hipStream_t stream) {
