@@ -4,8 +4,8 @@
 // program per token and copies the token's K row and V row (num_kv_heads * head_dim
 // elements each) into slot slot_mapping[i], skipping slot -1.
 //
-// Here a work-group moves the rows of a few consecutive tokens (8 tokens of a 2 KiB
-// row): a thread moves four 16-byte chunks of K rows and the matching chunks of the V
+// Here a work-group moves the rows of a few consecutive tokens (4 tokens of a 2 KiB
+// row): a thread moves two 16-byte chunks of K rows and the matching chunks of the V
 // rows, so a wavefront stores 1 KiB of contiguous cache row per operand and
 // instruction, with dwordx4 stores. The copy is a bit copy: results are identical to
 // the reference for any 16-bit dtype.
@@ -15,11 +15,17 @@ namespace pk {
 namespace {
 
 constexpr int kStoreThreads = 256;
-constexpr int kStoreUnroll = 4;  // 16-byte chunks per thread and round, loads issued together
+// 16-byte chunks per thread and round, loads issued together. Measured (cold caches, K and V
+// rows of 2 KiB, µs for 16384 / 2048 / 256 tokens): 2 chunks 26.2 / 7.4 / 6.2, 4 chunks
+// 26.9 / 8.6 / 7.0, 8 chunks 26.4 / 10.6 / 9.5; non-temporal loads of the new rows no faster.
+#ifndef PK_STORE_UNROLL
+#define PK_STORE_UNROLL 2
+#endif
+constexpr int kStoreUnroll = PK_STORE_UNROLL;
 constexpr int kStoreChunks = kStoreThreads * kStoreUnroll;  // chunks a work-group moves per round
 
 // Work-group x moves tokens [x * tokens_per_group, ...): its chunks are numbered i = token
-// offset * row_vec + chunk, and a round gives thread j chunks j, j + 256, j + 512, j + 768.
+// offset * row_vec + chunk, and a round gives thread j chunks j, j + 256, ....
 // The token of chunk i is i >> row_shift when the row is a power of two of chunks (every
 // head geometry with a power-of-two kv head count and head_dim 128), else a 32-bit
 // division. All slot loads of a round go out first, then all K and V loads (from a valid
@@ -92,7 +98,7 @@ hipError_t launch_store_kvcache(const void* key, int64_t key_row_stride, const v
   const int32_t row_vec = row_elems / 8;
   int32_t row_shift = -1;
   if ((row_vec & (row_vec - 1)) == 0) row_shift = __builtin_ctz((unsigned)row_vec);
-  // one round of 1024 chunks per work-group (8 tokens of a 2 KiB row), at least one token
+  // one round of kStoreChunks chunks per work-group (4 tokens of a 2 KiB row), at least one token
   const int32_t per_group = row_vec >= kStoreChunks ? 1 : kStoreChunks / row_vec;
   const int64_t groups = ((int64_t)num_tokens + per_group - 1) / per_group;
   hipLaunchKernelGGL(store_kvcache_kernel, dim3((unsigned)groups), dim3(kStoreThreads), 0, stream,
