@@ -228,6 +228,12 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf
       for (int rr = 0; rr < 16; ++rr) o[md][rr] *= alpha;
   }
   const float m_use = (m_i == -INFINITY) ? 0.f : m_i;  // row saw no key yet: every p is 0
+// The row sum l from the bf16 p that the P.V product uses (16 v_dot2 per row block and tile
+// instead of 32 fp32 adds): numerator and denominator then weigh every key alike. Measured
+// interleaved: steady batch 693.6 -> 680.2 us, cfg3 prefill 95.9 -> 95.4 us.
+#ifndef PK_PREFILL_DOT_SUM
+#define PK_PREFILL_DOT_SUM 1
+#endif
   float psum = 0.f;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
@@ -235,9 +241,8 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf
     for (int rr = 0; rr < 16; ++rr) {
       const float p = exp2_fast(__builtin_fmaf(s[mb][rr], scale_log2, -m_use));
       s[mb][rr] = p;
-      psum += p;
+      if (!PK_PREFILL_DOT_SUM) psum += p;
     }
-  l_i += psum;
   // B operand of k-block kb2: element e of lane half `half` stands for key
   // 16 kb2 + 8 (e >> 2) + 4 half + (e & 3) = accumulator element 8 (kb2 & 1) + e of
   // half-tile kb2 >> 1.
@@ -245,6 +250,18 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf
   for (int kb2 = 0; kb2 < 4; ++kb2)
 #pragma unroll
     for (int e = 0; e < 8; ++e) pb[kb2][e] = static_cast<__bf16>(s[kb2 >> 1][8 * (kb2 & 1) + e]);
+  if (PK_PREFILL_DOT_SUM) {
+    // the row sum from the bf16 p the P.V product uses: one v_dot2 per pair of keys
+    const bf16x2 one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+#pragma unroll
+    for (int kb2 = 0; kb2 < 4; ++kb2)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const bf16x2 pr = {pb[kb2][e], pb[kb2][e + 1]};
+        psum = __builtin_amdgcn_fdot2_f32_bf16(pr, one, psum, false);
+      }
+  }
+  l_i += psum;
 }
 
 // Per-lane LDS byte offsets of the MFMA operand reads inside a stage.
@@ -1237,7 +1254,10 @@ bool launch_shared_prefix_flat(AttnArgs& a, int group, hipStream_t stream, hipEr
   // decode work-groups fill the CUs beside the prefix ones; those take half a share after
   // their prefix work. The flat grid shrinks to the groups these hold (never grows: the
   // workspace's partial slots are sized for the flat plan's grid).
-  const int tail = per / 2;
+#ifndef PK_SP_TAIL_DIV
+#define PK_SP_TAIL_DIV 2
+#endif
+  const int tail = PK_SP_TAIL_DIV > 0 ? per / PK_SP_TAIL_DIV : 0;
   const int D = cus - (int)P;
   const int64_t total = (int64_t)D * per + P * tail;             // flat groups, recorder included
   const int W = (int)std::min<int64_t>(a.flat_groups, total - a.num_seqs - 1);
