@@ -227,7 +227,8 @@ def cpu_baselines(dev, gpu_kernels: dict | None, reps: int = 3) -> dict:
 
 
 def prefill_probe(dev) -> int:
-    """5 calls each of cfg3's prefill part and the prefill_steady batch (counter passes)."""
+    """5 calls each of cfg3's prefill part, the prefill_steady batch and the dense 16384-token
+    prompt batch (counter passes)."""
     import torch
 
     from pagedkv.workloads import make_workload
@@ -240,6 +241,11 @@ def prefill_probe(dev) -> int:
         torch.cuda.synchronize()
         log(f"[bench] prefill probe: {name} done")
         del w
+    fn, _, _ = dense_prefill_call(dev)
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    log("[bench] prefill probe: dense done")
     return 0
 
 
