@@ -196,9 +196,12 @@ int pk_varlen_attention_shared_prefix(const void* q, int64_t q_row_stride,
  * counterpart in the reference. Same arguments, semantics and kernels as
  * pk_varlen_attention_ex -- outputs are bit-identical -- minus the workspace: the split-K
  * partials and the prefill work plan live in a static device array of
- * PK_NOALLOC_SCRATCH_BYTES (128 MiB) that each GPU the library runs on holds from the
- * first call on it until the process ends. The call allocates nothing (no hipMalloc, no
- * allocating library routine).
+ * PK_NOALLOC_SCRATCH_BYTES (128 MiB) that each GPU holds from the first call on it until the
+ * process ends. The array is the only content of its own code object, which the HIP runtime
+ * (deferred code-object loading, its default) loads at the first address lookup: a process
+ * that never calls this entry point does not hold it (measured on MI355X: free device memory
+ * drops by 130 MiB at the first call, by none at the library's other launches). The call
+ * allocates nothing (no hipMalloc, no allocating library routine).
  *   - Launch bounds whose pk_varlen_attention_workspace_bytes exceeds the scratch return
  *     PK_ERR_WORKSPACE before any launch (every batch of the five benchmark shapes fits:
  *     256 decode sequences of up to 8192 keys need 32.5 MiB, a mixed chunked-prefill batch
