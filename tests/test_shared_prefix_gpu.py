@@ -244,3 +244,52 @@ def test_work_groups_take_several_groups_in_turn(gpu, hq, hkv):
     torch.cuda.synchronize()
     assert_close_bf16(out, want, f"six groups per window, hkv={hkv}")
     assert_close_bf16(plain, want, f"plain path, hkv={hkv}")
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 8), (16, 4), (32, 4), (16, 16), (24, 12), (2, 1)])
+def test_one_launch_prefix_and_flat_suffixes(gpu, hq, hkv):
+    """Batches whose suffixes take the flat decode grid run the prefix work and the suffix
+    grid in one launch: 150 sequences over a 1024-key shared prefix (two shapes of sharing:
+    all of it, and a branch sharing only its first block) with ragged suffixes, one sequence
+    ending inside the prefix, and graph padding. GQA groups 1-8; 16 kv heads (four wavefronts
+    per flat group), 12 (not a divisor of the work-group's wavefronts: two launches), and one.
+    Every row against the oracle; bit-identical to private copies of the prefix blocks."""
+    g = torch.Generator().manual_seed(hq * 100 + hkv)
+    tables, lens = [], []
+    nxt = 4
+    for i in range(150):
+        suffix = int(torch.randint(100, 1500, (1,), generator=g))
+        nb_s = math.ceil(suffix / BS)
+        head = [0, 1, 2, 3] if i % 5 else [0, 50000]                 # every fifth shares one block
+        if head[-1] == 50000:
+            head = [0, nxt]
+            nxt += 1
+        tables.append(head + list(range(nxt, nxt + nb_s)))
+        lens.append(len(head) * BS + suffix)
+        nxt += nb_s
+    tables.append([0, 1])
+    lens.append(BS + 77)                                              # ends inside the prefix
+    tables.append([])
+    lens.append(0)                                                    # graph padding
+    q_lens = [1] * (len(tables) - 1) + [0]
+    b = _batch(tables, lens, q_lens, hq, hkv, nxt, seed=hq * 10 + hkv, dev=gpu)
+    print(f"[shared prefix] one launch {hq}/{hkv}", flush=True)
+    want = _oracle(b)
+    out = _run(b, 4 * BS, hint=4 * BS)
+    torch.cuda.synchronize()
+    n = sum(q_lens)
+    assert_close_bf16(out[:n], want[:n], f"one launch {hq}/{hkv}")
+    # private copies of blocks 0-3 per sequence: the same bits
+    kc, vc, bt = b["kc"], b["vc"], b["bt"].clone()
+    nb = kc.shape[0]
+    extra = []
+    for i in range(len(tables)):
+        for j, blk in enumerate(tables[i][:4]):
+            if blk < 4:
+                bt[i, j] = nb + len(extra)
+                extra.append(blk)
+    idx = torch.tensor(extra, device=gpu)
+    b2 = dict(b, kc=torch.cat([kc, kc[idx]]), vc=torch.cat([vc, vc[idx]]), bt=bt)
+    priv = _run(b2, 4 * BS, hint=4 * BS)
+    torch.cuda.synchronize()
+    assert bits_equal(out[:n], priv[:n])
