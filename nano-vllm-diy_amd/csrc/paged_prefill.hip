@@ -82,6 +82,7 @@ constexpr int kMergeLoads = PK_MERGE_LOADS;  // merge: splits whose outputs load
 #endif
 constexpr int kBuckets = PK_PREFILL_BUCKETS;  // length buckets of the work list (longest first)
 constexpr float kLazyLog2 = 8.f;       // reference max moves only when exceeded by 2^8
+constexpr int kStages = 2;             // K and V LDS stages of the prefill kernel
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
@@ -135,7 +136,7 @@ constexpr int kRowsPerWave = kTileKeys / kPrefillWaves;
 constexpr int kLoadsPerOperand = kRowsPerWave / 4;
 
 
-// Per-lane source offsets (elements) of the rows this lane moves.
+// Per-lane source byte offsets of the rows this lane moves.
 struct LoadLanes {
   int k[kLoadsPerOperand];
   int v[kLoadsPerOperand];
@@ -148,8 +149,8 @@ __device__ __forceinline__ LoadLanes load_lanes(const AttnArgs& a, int wave, int
   for (int i = 0; i < kLoadsPerOperand; ++i) {
     const int r = kRowsPerWave * wave + 4 * i + (lane >> 4);  // tile row this lane fills
     const int rs = min(r, last);                              // source row (clamped on the last tile)
-    l.k[i] = rs * (int)a.k_row_stride + (slot ^ (r & 15)) * 8;
-    l.v[i] = rs * (int)a.v_row_stride + v_chunk(r, slot) * 8;
+    l.k[i] = (rs * (int)a.k_row_stride + (slot ^ (r & 15)) * 8) * 2;
+    l.v[i] = (rs * (int)a.v_row_stride + v_chunk(r, slot) * 8) * 2;
   }
   return l;
 }
@@ -158,6 +159,18 @@ struct KvRegs {
   u32x4 k[kLoadsPerOperand];
   u32x4 v[kLoadsPerOperand];
 };
+
+// The lane's 16-byte loads of one tile from K and V rows starting at kbase / vbase. (Buffer
+// loads over the tile's rows, which keep no 64-bit lane address, measured 2-4% slower on
+// the prefill batches.)
+__device__ __forceinline__ void load_rows(const uint16_t* kbase, const uint16_t* vbase, const LoadLanes& l,
+                                          KvRegs& R) {
+#pragma unroll
+  for (int i = 0; i < kLoadsPerOperand; ++i) {
+    R.k[i] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kbase) + l.k[i]);
+    R.v[i] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(vbase) + l.v[i]);
+  }
+}
 
 template <bool PAGED>
 __device__ __forceinline__ void load_tile_regs(const AttnArgs& a, int b, int k0, int Lk, int g, int bt_lane, int wave,
@@ -177,12 +190,7 @@ __device__ __forceinline__ void load_tile_regs(const AttnArgs& a, int b, int k0,
   }
   kbase += g * kHeadDim;
   vbase += g * kHeadDim;
-  const LoadLanes l = (t0 + kTileKeys <= Lk) ? full_lanes : load_lanes(a, wave, lane, Lk - 1 - t0);
-#pragma unroll
-  for (int i = 0; i < kLoadsPerOperand; ++i) {
-    R.k[i] = *reinterpret_cast<const u32x4*>(kbase + l.k[i]);
-    R.v[i] = *reinterpret_cast<const u32x4*>(vbase + l.v[i]);
-  }
+  load_rows(kbase, vbase, (t0 + kTileKeys <= Lk) ? full_lanes : load_lanes(a, wave, lane, Lk - 1 - t0), R);
 }
 
 __device__ __forceinline__ void store_tile_lds(const KvRegs& R, lds_char* kdst, lds_char* vdst, int wave, int lane) {
@@ -202,21 +210,31 @@ __device__ __forceinline__ void store_tile_lds(const KvRegs& R, lds_char* kdst, 
 // moves only when some row's tile max exceeds it by more than kLazyLog2; then every row
 // moves to its running max and the numerator and sum are rescaled. p <= 2^kLazyLog2, and
 // numerator and sum share the reference, so o / l is unchanged.
-__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf16x8 (&pb)[4], float& m_i, float& l_i,
-                                              int t0, int lim, bool full, float scale_log2, int half) {
-  if (!full) {
+// The parts of softmax_block over NB half-tiles of 32 keys (element rr of half-tile mb is
+// key t0 + 32 mb + 8 (rr >> 2) + 4 half + (rr & 3)): the mask (diagonal tiles) and the
+// row's max in the exp2 domain ...
+template <int NB>
+__device__ __forceinline__ void softmax_mask(f32x16 (&s)[NB], int t0, int lim, int half) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+  for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr)
-        if (t0 + mb * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3) > lim) s[mb][rr] = -INFINITY;
-  }
+    for (int rr = 0; rr < 16; ++rr)
+      if (t0 + mb * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3) > lim) s[mb][rr] = -INFINITY;
+}
+
+template <int NB, bool MASK>
+__device__ __forceinline__ float softmax_max(f32x16 (&s)[NB], int t0, int lim, float scale_log2, int half) {
+  if constexpr (MASK) softmax_mask<NB>(s, t0, lim, half);
   float tmax = -INFINITY;
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
+  for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) tmax = fmaxf(tmax, s[mb][rr]);
-  const float tm = swap_halves_max(tmax) * scale_log2;
+  return swap_halves_max(tmax) * scale_log2;
+}
+
+// ... the lazy move of the reference max (with the rescale of numerator and sum) ...
+__device__ __forceinline__ void softmax_rescale(f32x16 (&o)[4], float& m_i, float& l_i, float tm) {
   if (__builtin_amdgcn_ballot_w64(tm > m_i + kLazyLog2) != 0) {
     const float m_new = fmaxf(m_i, tm);
     const float alpha = m_new == -INFINITY ? 1.f : exp2_fast(m_i - m_new);  // 0 when m_i = -inf
@@ -227,16 +245,22 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) o[md][rr] *= alpha;
   }
-  const float m_use = (m_i == -INFINITY) ? 0.f : m_i;  // row saw no key yet: every p is 0
+}
+
 // The row sum l from the bf16 p that the P.V product uses (16 v_dot2 per row block and tile
 // instead of 32 fp32 adds): numerator and denominator then weigh every key alike. Measured
 // interleaved: steady batch 693.6 -> 680.2 us, cfg3 prefill 95.9 -> 95.4 us.
 #ifndef PK_PREFILL_DOT_SUM
 #define PK_PREFILL_DOT_SUM 1
 #endif
+// ... and the exponentials against the reference max, packed to bf16 as the P.V B operand.
+template <int NB>
+__device__ __forceinline__ void softmax_exp(f32x16 (&s)[NB], bf16x8 (&pb)[2 * NB], float m_i, float& l_i,
+                                            float scale_log2) {
+  const float m_use = (m_i == -INFINITY) ? 0.f : m_i;  // row saw no key yet: every p is 0
   float psum = 0.f;
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
+  for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const float p = exp2_fast(__builtin_fmaf(s[mb][rr], scale_log2, -m_use));
@@ -247,14 +271,14 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf
   // 16 kb2 + 8 (e >> 2) + 4 half + (e & 3) = accumulator element 8 (kb2 & 1) + e of
   // half-tile kb2 >> 1.
 #pragma unroll
-  for (int kb2 = 0; kb2 < 4; ++kb2)
+  for (int kb2 = 0; kb2 < 2 * NB; ++kb2)
 #pragma unroll
     for (int e = 0; e < 8; ++e) pb[kb2][e] = static_cast<__bf16>(s[kb2 >> 1][8 * (kb2 & 1) + e]);
   if (PK_PREFILL_DOT_SUM) {
     // the row sum from the bf16 p the P.V product uses: one v_dot2 per pair of keys
     const bf16x2 one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 #pragma unroll
-    for (int kb2 = 0; kb2 < 4; ++kb2)
+    for (int kb2 = 0; kb2 < 2 * NB; ++kb2)
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         const bf16x2 pr = {pb[kb2][e], pb[kb2][e + 1]};
@@ -264,14 +288,26 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf
   l_i += psum;
 }
 
+__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[4], bf16x8 (&pb)[4], float& m_i, float& l_i,
+                                              int t0, int lim, bool full, float scale_log2, int half) {
+  const float tm = full ? softmax_max<2, false>(s, t0, lim, scale_log2, half)
+                        : softmax_max<2, true>(s, t0, lim, scale_log2, half);
+  softmax_rescale(o, m_i, l_i, tm);
+  softmax_exp<2>(s, pb, m_i, l_i, scale_log2);
+}
+
 // Per-lane LDS byte offsets of the MFMA operand reads inside a stage.
 //   K, k-block kb: row col (+ 32 for the second half-tile: + 8 KiB), chunk 2 kb + half,
 //     swizzled with col & 15 (32 mb + col has the same low bits);
 //   V, d-block md: row 4 half + (src >> 2) (+ 16 kb2 rows: + 4 KiB, + 8 rows: + 2 KiB), the
 //     swizzle (2 r) & 15 does not see those row steps.
 struct TileLanes {
-  int k[kHeadDim / 16];
-  int v[4];
+  int k0, v0;
+  // Offsets of k-block kb and d-block md: the k-block moves the chunk by 2 kb and the d-block
+  // by 4 md, bits the swizzles only XOR with lane bits, so the offsets are k0 ^ 32 kb and
+  // v0 ^ 64 md (one VALU op per read instead of twelve live registers).
+  __device__ __forceinline__ int k(int kb) const { return k0 ^ (32 * kb); }
+  __device__ __forceinline__ int v(int md) const { return v0 ^ (64 * md); }
 };
 
 __device__ __forceinline__ TileLanes tile_lanes(int lane) {
@@ -280,14 +316,10 @@ __device__ __forceinline__ TileLanes tile_lanes(int lane) {
   const int half = lane >> 5;
   const int grp = lane >> 4;
   const int src = lane & 15;
-#pragma unroll
-  for (int kb = 0; kb < kHeadDim / 16; ++kb) t.k[kb] = col * kRowBytes + k_slot(col, 2 * kb + half) * 16;
-#pragma unroll
-  for (int md = 0; md < 4; ++md) {
-    const int d = md * 32 + 16 * (grp & 1) + 4 * (src & 3);
-    const int r = 4 * half + (src >> 2);
-    t.v[md] = r * kRowBytes + v_slot(r, d >> 3) * 16 + (d & 7) * 2;
-  }
+  t.k0 = col * kRowBytes + k_slot(col, half) * 16;
+  const int d = 16 * (grp & 1) + 4 * (src & 3);
+  const int r = 4 * half + (src >> 2);
+  t.v0 = r * kRowBytes + v_slot(r, d >> 3) * 16 + (d & 7) * 2;
   return t;
 }
 
@@ -318,7 +350,7 @@ __device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char*
   const auto read_k = [&](int kb) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
-      ka[kb][mb] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(sK + tl.k[kb] +
+      ka[kb][mb] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(sK + tl.k(kb) +
                                                                                    mb * 32 * kRowBytes);
   };
 #pragma unroll
@@ -354,7 +386,7 @@ __device__ __forceinline__ void compute_tile(const lds_char* sK, const lds_char*
   for (int kb2 = 0; kb2 < 4; ++kb2) {
 #pragma unroll
     for (int md = 0; md < 4; ++md) {
-      const lds_char* p_lo = sV + tl.v[md] + kb2 * 16 * kRowBytes;
+      const lds_char* p_lo = sV + tl.v(md) + kb2 * 16 * kRowBytes;
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           const_cast<lds_v4i16*>(reinterpret_cast<const lds_v4i16*>(p_lo)));
       const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -519,7 +551,8 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const AttnAr
 // after the last tile's barrier (before the epilogue), after_epilogue after its stores.
 template <int G, bool PAGED, bool CAUSAL, class LastStep, class AfterTiles, class AfterEpilogue>
 __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, const int g, const int cuv,
-                                             const int bt_lane, lds_char* const (&KS)[2], lds_char* const (&VS)[2],
+                                             const int bt_lane, lds_char* const (&KS)[kStages],
+                                             lds_char* const (&VS)[kStages],
                                              int wave, int lane,
                                              LastStep&& last_step, AfterTiles&& after_tiles,
                                              AfterEpilogue&& after_epilogue) {
@@ -677,13 +710,13 @@ __device__ __forceinline__ void prefill_item(const AttnArgs& a, const int4 it, c
 template <int G, bool PAGED, bool CAUSAL>
 __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void prefill_kernel(const AttnArgs a) {
   // two stages per operand (constant stage indices put the stage offset in immediates)
-  __shared__ __attribute__((aligned(1024))) char sK[2][kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char sV[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sK[kStages][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char sV[kStages][kTileBytes];
   __shared__ int s_item;  // the claimed item index
-  lds_char* KS[2];
-  lds_char* VS[2];
+  lds_char* KS[kStages];
+  lds_char* VS[kStages];
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
+  for (int st = 0; st < kStages; ++st) {
     KS[st] = (lds_char*)sK[st];
     VS[st] = (lds_char*)sV[st];
   }
@@ -1045,12 +1078,7 @@ __device__ __forceinline__ void shared_prefix_work(const AttnArgs& a, const int 
       const int off = t0 % BS;
       const uint16_t* kbase = a.k + (int64_t)id * a.k_block_stride + (int64_t)off * a.k_row_stride + g * D;
       const uint16_t* vbase = a.v + (int64_t)id * a.v_block_stride + (int64_t)off * a.v_row_stride + g * D;
-      const LoadLanes l = load_lanes(a, wave, lane, min(kTileKeys, cnt - 1 - t0));
-#pragma unroll
-      for (int j = 0; j < kLoadsPerOperand; ++j) {
-        R.k[j] = *reinterpret_cast<const u32x4*>(kbase + l.k[j]);
-        R.v[j] = *reinterpret_cast<const u32x4*>(vbase + l.v[j]);
-      }
+      load_rows(kbase, vbase, load_lanes(a, wave, lane, min(kTileKeys, cnt - 1 - t0)), R);
     };
     // the first two tiles are requested before the members and their q rows (which depend
     // on the member list), so the three rounds of loads overlap
