@@ -267,6 +267,10 @@ def main() -> int:
                     help="only run 5 calls of one workload (default: the cfg2 decode call) and 5 copies "
                          "of 1 GiB (the counter calibration), for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
                          "passes")
+    ap.add_argument("--call-probe", default=None,
+                    help="only run 5 cold-cache calls of each named workload (comma-separated: cfg2, "
+                         "cfg2_tp2/4/8, cfg4, decode_serve, cfg3, cfg3_prefill, prefill_steady, dense_prefill, "
+                         "store_16384), one at a time, for a rocprofv3 --kernel-trace of each call's launches")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the paged-KV path is not sharded across GPUs "
@@ -287,6 +291,8 @@ def main() -> int:
         return prefill_probe(dev)
     if args.pmc_probe:
         return pmc_probe(dev, args.pmc_probe)
+    if args.call_probe:
+        return call_probe(dev, args.call_probe.split(","))
     log("[bench] building cfg2 (256 seqs, Lk ~ U[1024, 8192]) on the GPU")
     w = make_workload("cfg2", dev)
     kv_bytes = w.decode_kv_bytes()
@@ -451,6 +457,36 @@ def pmc_probe(dev, name: str) -> int:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_probe": name, **info, "copy_bytes": 1 << 30}), flush=True)
+    return 0
+
+
+def call_probe(dev, names) -> int:
+    """Per workload: one warm call, then 5 calls each after a cache flush and followed by a
+    synchronize, so a kernel trace shows every launch of one call (and the gaps between them)
+    on its own."""
+    import torch
+
+    from pagedkv.workloads import TP_HEADS, make_workload
+
+    for name in names:
+        if name == "store_16384":
+            fn = store_call(dev, 16384)[0]
+        elif name == "dense_prefill":
+            fn = dense_prefill_call(dev)[0]
+        elif name == "cfg3_prefill":
+            w = make_workload("cfg3", dev)
+            fn = attention_call(w, sub_batch(w, lambda i: w.q_lens[i] > 1))
+        else:
+            base, _, tp = name.partition("_tp")
+            fn = attention_call(make_workload(base, dev, heads=TP_HEADS[int(tp) if tp else 1]))
+        fn()
+        torch.cuda.synchronize()
+        for _ in range(5):
+            flush_caches()
+            torch.cuda.synchronize()
+            fn()
+            torch.cuda.synchronize()
+        print(json.dumps({"call_probe": name, "calls": 5}), flush=True)
     return 0
 
 

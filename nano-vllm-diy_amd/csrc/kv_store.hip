@@ -17,7 +17,9 @@ namespace {
 constexpr int kStoreThreads = 256;
 // 16-byte chunks per thread and round, loads issued together. Measured (cold caches, K and V
 // rows of 2 KiB, µs for 16384 / 2048 / 256 tokens): 2 chunks 26.2 / 7.4 / 6.2, 4 chunks
-// 26.9 / 8.6 / 7.0, 8 chunks 26.4 / 10.6 / 9.5; non-temporal loads of the new rows no faster.
+// 26.9 / 8.6 / 7.0, 8 chunks 26.4 / 10.6 / 9.5; non-temporal loads of the new rows no faster;
+// non-temporal cache stores 26.5 -> 29.8 at 16384 tokens; two or four rounds per work-group
+// (fewer, longer work-groups) 28.0 and 26.8 at 16384 tokens, slower at 2048 and 256.
 #ifndef PK_STORE_UNROLL
 #define PK_STORE_UNROLL 2
 #endif
