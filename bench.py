@@ -267,6 +267,8 @@ def main() -> int:
                     help="only run 5 calls of one workload (default: the cfg2 decode call) and 5 copies "
                          "of 1 GiB (the counter calibration), for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
                          "passes")
+    ap.add_argument("--no-pmc", action="store_true",
+                    help="take roofline.traffic from profiles/traffic.json instead of measuring it")
     ap.add_argument("--call-probe", default=None,
                     help="only run 5 cold-cache calls of each named workload (comma-separated: cfg2, "
                          "cfg2_tp2/4/8, cfg4, decode_serve, cfg3, cfg3_prefill, prefill_steady, dense_prefill, "
@@ -333,12 +335,20 @@ def main() -> int:
     achieved = kv_bytes / (attn_mean * 1e-3) / 1e9
     log(f"[bench] step {ms_per_step:.3f} ms, decode call {attn_mean:.3f} ms -> {achieved:.1f} GB/s")
 
-    # HBM bytes per decode call on this workload, measured with rocprofv3 --pmc
-    # FETCH_SIZE / WRITE_SIZE (calibrated on a copy of known size); recorded in profiles/
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("cfg2_decode_call_hbm_bytes")
+    # HBM bytes per decode call on this workload: two rocprofv3 --pmc passes (FETCH_SIZE,
+    # WRITE_SIZE) run now, in child processes; if the profiler is missing or a pass fails, the
+    # value recorded in profiles/ by the same passes
+    traffic, traffic_source = None, None
+    if not args.no_pmc:
+        log("[bench] HBM traffic of the decode call: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+        traffic, traffic_source = pmc_traffic("cfg2")
+    if traffic is None:
+        tfile = ROOT / "profiles" / "traffic.json"
+        if tfile.exists():
+            traffic = json.loads(tfile.read_text()).get("cfg2_decode_call_hbm_bytes")
+            traffic_source = (f"profiles/traffic.json (recorded by the same passes; a pass in this run: "
+                              f"{traffic_source or 'skipped'})")
+    log(f"[bench] traffic {traffic} B per call ({traffic_source})")
 
     result = {
         "metric": METRIC,
@@ -370,6 +380,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_over_algorithmic": round(traffic / kv_bytes, 4) if traffic else None,
+            "traffic_source": traffic_source,
             "launch_ms_mean": round(attn_mean, 4),
             "launch_ms_median": round(statistics.median(attn_ms), 4),
         },
@@ -458,6 +470,77 @@ def pmc_probe(dev, name: str) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"pmc_probe": name, **info, "copy_bytes": 1 << 30}), flush=True)
     return 0
+
+
+def pmc_traffic(name: str, timeout_s: float = 150.0):
+    """HBM bytes per call of one workload's path, measured now: rocprofv3 --pmc FETCH_SIZE,
+    then WRITE_SIZE, each over a child `bench.py --pmc-probe NAME` (6 calls of the path, then
+    5 device copies of 1 GiB). Each counter's per-dispatch value (KiB) for the path's kernels
+    is scaled by the factor that makes it read 1 GiB for the copies, and the per-dispatch
+    means of the path's kernels are summed (one launch of each per call). Returns
+    (bytes, how) or (None, why not). A pass that does not finish in timeout_s is killed with
+    its process group."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    scaled, factors = {}, {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory(dir="/tmp") as d:
+            cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "p", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--pmc-probe", name]
+            try:
+                p = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                                     stderr=subprocess.DEVNULL, start_new_session=True)
+            except OSError as e:
+                return None, f"{counter} pass not started ({e})"
+            try:
+                p.wait(timeout=timeout_s)
+            except subprocess.TimeoutExpired:
+                os.killpg(p.pid, signal.SIGKILL)
+                p.wait()
+                return None, f"{counter} pass killed after {timeout_s:.0f} s"
+            # (the profiler may exit non-zero after writing whole results: the CSV decides)
+            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+            if not files:
+                return None, f"{counter} pass wrote no counters (exit {p.returncode})"
+            with open(files[0]) as f:
+                got = pmc_call_bytes(csv.DictReader(f), counter)
+        if got is None:
+            return None, f"{counter} pass: no path or copy dispatches in the counters"
+        scaled[counter], factors[counter] = got
+    total = int(round(scaled["FETCH_SIZE"] + scaled["WRITE_SIZE"]))
+    return total, (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes in this run over bench.py --pmc-probe "
+                   f"{name}: {scaled['FETCH_SIZE']:.0f} B read + {scaled['WRITE_SIZE']:.0f} B written per call "
+                   f"(factors {factors['FETCH_SIZE']} / {factors['WRITE_SIZE']} from the 1 GiB copies)")
+
+
+def pmc_call_bytes(rows, counter: str):
+    """(bytes per call, factor) from rocprofv3 counter rows of a --pmc-probe run: the mean
+    per-dispatch value (KiB) of each library kernel, summed over the kernels, times the factor
+    that makes the large device copies (the probe's 1 GiB copies: the copy dispatches of at
+    least half the largest one's count) read or write 1 GiB. None without such rows."""
+    per_kernel, copies = {}, []
+    for r in rows:
+        if r.get("Counter_Name") != counter:
+            continue
+        v = float(r["Counter_Value"])
+        k = r["Kernel_Name"]
+        if "pk::" in k:
+            per_kernel.setdefault(k, []).append(v)
+        elif "copyBuffer" in k:
+            copies.append(v)
+    big = [v for v in copies if v >= 0.5 * max(copies)] if copies else []
+    if not per_kernel or not big or statistics.median(big) <= 0:
+        return None
+    factor = (1 << 30) / (statistics.median(big) * 1024)
+    return sum(statistics.fmean(v) for v in per_kernel.values()) * 1024 * factor, round(factor, 4)
 
 
 def call_probe(dev, names) -> int:
