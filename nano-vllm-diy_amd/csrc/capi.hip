@@ -688,8 +688,10 @@ int pk_linear_add_rmsnorm(const void* x, int64_t x_row_stride, const void* weigh
 
 // ---- allocation-free entry point --------------------------------------------------------
 // pk_varlen_attention_noalloc runs the kernels of pk_varlen_attention_ex on this file-scope
-// device array instead of a caller's workspace. Each GPU the library runs on holds its own
-// copy (PK_NOALLOC_SCRATCH_BYTES) from the first launch on it until the process ends. In host
+// device array instead of a caller's workspace. Each GPU holds its own copy
+// (PK_NOALLOC_SCRATCH_BYTES) from the first call of this entry point on it until the process
+// ends: the array is the only device content of this file's code object, which loads at the
+// symbol lookup below, not at the library's other launches. In host
 // code `scratch` names a host-side stand-in, not device memory: its device address comes from
 // hipGetSymbolAddress, once per device with that device current, and only that address is
 // ever passed to a kernel.
