@@ -71,6 +71,18 @@ struct DecodeState {
   float acc[G][8];    // running P.V numerator (this lane's 8 elements)
 };
 
+// Cache block ids of a unit's keys, one per lane (lane i: table entry blk0 + i), loaded once
+// before its pipeline when BR is set, so that a step's block id is a readlane instead of a
+// scalar load that the step waits for before its K/V loads go out. A unit spanning more than a
+// wavefront's worth of blocks reads the table per step. Used where it measured faster: the
+// flat groups of the shared-prefix launch (cfg4 41.9 -> 40.3 us, interleaved); in the split
+// and flat decode kernels it measured slower on cfg2 (748.7 -> 757.9 us) and cfg1.
+struct UnitBlocks {
+  int ids;      // this lane's block id
+  int blk0;     // the unit's first table entry
+  bool in_regs;
+};
+
 // Issue the K then V loads of keys [t, t + U) of this lane's kv head. lane_bytes is the
 // lane's byte offset inside a token row. Keys past t_end re-read the step's last valid
 // row (same cache block, finite data) and consume() masks them to p = 0, so no load
@@ -101,15 +113,18 @@ __device__ __forceinline__ int scalar_block_id(const int32_t* row, int j) {
 // go out (the pipeline's wait counts stay exact) over an empty buffer range, so they return
 // zeros without touching memory (a re-read of the last step, streamed past L2, came back from
 // HBM: one extra step per unit, ~15% of the bytes of a short flat-grid piece).
-template <int U, int R, bool PAGED, bool STREAM, bool FUSED>
+template <int U, int R, bool PAGED, bool STREAM, bool FUSED, bool BR>
 __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_k, uint32_t lane_v, int b, int k0, int t,
-                                            int t_end, bool live, u32x4 (&kr)[U], u32x4 (&vr)[U]) {
+                                            int t_end, bool live, const UnitBlocks& ub, u32x4 (&kr)[U],
+                                            u32x4 (&vr)[U]) {
   const uint16_t* kp;
   const uint16_t* vp;
   if constexpr (PAGED) {
     // [t, t + U R) lies inside one cache block: U R divides block_size and split_tokens.
-    const int blk = FUSED ? scalar_block_id(a.block_table + (int64_t)b * a.bt_stride, t / a.block_size)
-                          : a.block_table[(int64_t)b * a.bt_stride + t / a.block_size];
+    const int jb = t / a.block_size;
+    const int blk = (BR && ub.in_regs) ? __builtin_amdgcn_readlane(ub.ids, jb - ub.blk0)
+                    : FUSED            ? scalar_block_id(a.block_table + (int64_t)b * a.bt_stride, jb)
+                                       : a.block_table[(int64_t)b * a.bt_stride + jb];
     const int off = t % a.block_size;
     kp = a.k + (int64_t)blk * a.k_block_stride + (int64_t)off * a.k_row_stride;
     vp = a.v + (int64_t)blk * a.v_block_stride + (int64_t)off * a.v_row_stride;
@@ -145,7 +160,7 @@ __device__ __forceinline__ void issue_loads(const AttnArgs& a, uint32_t lane_k, 
 // stay exact. The scheduling barriers keep each step's loads together
 // ahead of its math: otherwise the scheduler sinks every load next to its first use to
 // save registers, which serialises their latency.
-template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, class Pre>
+template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, bool BR, class Pre>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_k, uint32_t lane_v,
                                              int j, int b, int k0, int t_begin, int t_end, Pre&& pre);
 
@@ -218,24 +233,32 @@ __device__ __forceinline__ void consume(DecodeState<G>& st, float c2, int t, int
   }
 }
 
-template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, class Pre>
+template <int G, int U, int R, bool PAGED, bool STREAM, bool FUSED, bool BR, class Pre>
 __device__ __forceinline__ void decode_range(DecodeState<G>& st, const AttnArgs& a, uint32_t lane_k, uint32_t lane_v,
                                              int j, int b, int k0, int t_begin, int t_end, Pre&& pre) {
   constexpr int S = U * R;  // keys per step
   const float c2 = a.scale_log2;
+  UnitBlocks ub{0, 0, false};
+  if constexpr (PAGED && BR) {
+    ub.blk0 = t_begin / a.block_size;
+    const int nblk = (t_end - 1) / a.block_size - ub.blk0 + 1;
+    ub.in_regs = nblk <= kWave;
+    const int lane = __lane_id();
+    if (ub.in_regs && lane < nblk) ub.ids = a.block_table[(int64_t)b * a.bt_stride + ub.blk0 + lane];
+  }
   u32x4 kA[U], vA[U], kB[U], vB[U];
-  issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t_begin, t_end, true, kA, vA);
+  issue_loads<U, R, PAGED, STREAM, FUSED, BR>(a, lane_k, lane_v, b, k0, t_begin, t_end, true, ub, kA, vA);
   pre();  // q (loaded or computed) while the first K/V loads are in flight
   for (int t = t_begin; t < t_end; t += 2 * S) {
     const int t1 = t + S;
-    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t1 < t_end ? t1 : t, t_end, t1 < t_end, kB,
-                                            vB);
+    issue_loads<U, R, PAGED, STREAM, FUSED, BR>(a, lane_k, lane_v, b, k0, t1 < t_end ? t1 : t, t_end, t1 < t_end, ub,
+                                                kB, vB);
     __builtin_amdgcn_sched_barrier(0);
     consume<G, U, R>(st, c2, t, t_end, j, kA, vA);
     if (t1 >= t_end) break;
     const int t2 = t1 + S;
-    issue_loads<U, R, PAGED, STREAM, FUSED>(a, lane_k, lane_v, b, k0, t2 < t_end ? t2 : t1, t_end, t2 < t_end, kA,
-                                            vA);
+    issue_loads<U, R, PAGED, STREAM, FUSED, BR>(a, lane_k, lane_v, b, k0, t2 < t_end ? t2 : t1, t_end, t2 < t_end, ub,
+                                                kA, vA);
     __builtin_amdgcn_sched_barrier(0);
     consume<G, U, R>(st, c2, t1, t_end, j, kB, vB);
   }
@@ -338,7 +361,7 @@ __device__ __forceinline__ void fused_producer(const AttnArgs& a, DecodeState<G>
 // leaves its (max, sum, numerator) partial at partial unit unit0 (x num_heads) for the combine.
 // R key rows per kv head: DPP row r holds kv head g_first + r mod (4 / R) and keys
 // t + u R + r / (4 / R) of every step; the rows of a head merge their states at the end.
-template <int G, int U, int R, bool PAGED, bool FUSED>
+template <int G, int U, int R, bool PAGED, bool FUSED, bool BR = false>
 __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_first, int b, int q0, int k0, int Lk,
                                             int t_begin, int t_end, bool direct, int64_t unit0) {
   static_assert(U % 2 == 0, "P.V pairs keys");
@@ -395,13 +418,13 @@ __device__ __forceinline__ void decode_unit(const AttnArgs& a, int lane, int g_f
   if (FUSED && t_end == Lk) {  // the split holding the token: store its K/V row first
     fused_producer<G>(a, st, q0, g, c, writer, true);
     if (stream)
-      decode_range<G, U, R, PAGED, true, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, nothing);
+      decode_range<G, U, R, PAGED, true, FUSED, BR>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, nothing);
     else
-      decode_range<G, U, R, PAGED, false, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, nothing);
+      decode_range<G, U, R, PAGED, false, FUSED, BR>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, nothing);
   } else if (stream) {
-    decode_range<G, U, R, PAGED, true, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, load_q);
+    decode_range<G, U, R, PAGED, true, FUSED, BR>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, load_q);
   } else {
-    decode_range<G, U, R, PAGED, false, FUSED>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, load_q);
+    decode_range<G, U, R, PAGED, false, FUSED, BR>(st, a, lane_k, lane_v, j, b, k0, t_begin, t_end, load_q);
   }
   merge_key_rows<G, R>(st, c2);
 
@@ -466,7 +489,7 @@ constexpr int kFlatSlots = 8;
 // the flat decode kernel runs it with u = its work-group index, the shared-prefix launch that
 // carries the flat grid with u numbered across its decode work-groups. `recorder`: this
 // wavefront records the line (chunk and every pos_b) for the combine if u is the last group.
-template <int G, int U, int R, bool PAGED, bool FUSED>
+template <int G, int U, int R, bool PAGED, bool FUSED, bool BR = false>
 __device__ __forceinline__ void flat_decode_piece(const AttnArgs& a, int u, int g_first, int lane, bool recorder) {
   constexpr int ST = U * R;  // keys per pipeline step: the line's step
   const int n = a.num_seqs;
@@ -531,8 +554,8 @@ __device__ __forceinline__ void flat_decode_piece(const AttnArgs& a, int u, int 
   const int t_end = min(Lk, Pb + (F1 - p0 + ST - 1) / ST * ST);
   // the sequence's first and last steps in one run and no prefix partial: this piece is all of it
   const bool direct = Pb == 0 && p0 / chunk == (p0 + (cb - 1) / ST * ST) / chunk;
-  decode_unit<G, U, R, PAGED, FUSED>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
-                                     ((int64_t)a.flat_unit0 + u) * a.num_heads);
+  decode_unit<G, U, R, PAGED, FUSED, BR>(a, lane, g_first, b, q0, k0, Lk, t_begin, t_end, direct,
+                                         ((int64_t)a.flat_unit0 + u) * a.num_heads);
 }
 
 // Merge the per-split partials of one (sequence, head). A separate pass (rather than a "last

@@ -1193,7 +1193,7 @@ __global__ __launch_bounds__(kPrefillThreads, kWavesPerSimd) void shared_prefix_
   const int qd = wave - j * a.sp_quads;
   const int u = first + j;
   if (j < count && u <= a.flat_groups + a.num_seqs)
-    flat_decode_piece<G, U, R, true, false>(a, u, qd * (4 / R), lane, qd == 0);
+    flat_decode_piece<G, U, R, true, false, true>(a, u, qd * (4 / R), lane, qd == 0);
 }
 
 
